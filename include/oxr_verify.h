@@ -1,0 +1,124 @@
+/*
+ * oxr_verify.h -- C ABI of the MI355X (gfx950) speculative-decoding verify step.
+ *
+ * Every entry point takes device pointers that the caller owns, plain sizes and
+ * a HIP stream (a `hipStream_t`, e.g. torch.cuda.current_stream().cuda_stream).
+ * They allocate nothing, never synchronize the device, and are safe to record
+ * into a HIP graph.  bf16 tensors are passed as `uint16_t` bit patterns.
+ *
+ * Return value: OXR_OK (0) on success; a negative OXR_ERR_* code when an
+ * argument is rejected before any launch; a positive hipError_t when a launch
+ * failed.  oxr_status_string() names each code.
+ *
+ * Reference interfaces each entry point replaces are cited as file:line in
+ * NickWilde18/oxr-inference (oxr_runtime/...).
+ */
+#ifndef OXR_VERIFY_H
+#define OXR_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OXR_ABI_VERSION 1
+
+#define OXR_OK 0
+#define OXR_ERR_INVALID_ARG (-1)   /* null pointer, negative or inconsistent size */
+#define OXR_ERR_UNSUPPORTED (-2)   /* shape outside what the kernels implement     */
+#define OXR_ERR_WORKSPACE (-3)     /* workspace missing or smaller than required   */
+
+typedef void* oxr_stream_t; /* hipStream_t */
+typedef uint16_t oxr_bf16;  /* raw bfloat16 bits */
+
+/* Library identity and status strings (no reference counterpart). */
+int oxr_abi_version(void);
+const char* oxr_status_string(int status);
+
+/*
+ * Self-test of the MFMA 16x16x32 bf16 operand layout the kernels assume (no
+ * reference counterpart): c[16x16] = a[16x32] @ b[32x16], bf16 in, fp32 out.
+ */
+int oxr_selftest_mfma_layout(const uint16_t* a, const uint16_t* b, float* c, oxr_stream_t stream);
+
+/*
+ * (1) Batched n-gram suffix-match drafting.
+ * Replaces NgramProposer.__init__/_add/extend/propose (oxr_runtime/speculative.py:15-39):
+ * for each sequence b with history h = history[b, :history_len[b]] and
+ * L = history_len[b], try n = min(max_n, L) .. 1 and take the largest p in
+ * [n, L-1] with h[p-n:p] == h[L-n:L]; the draft is h[p : min(p+k_b, L)] with
+ * k_b = k_limit ? max(0, min(k, k_limit[b])) : k.  No match -> empty draft.
+ * history is int32 [batch, history_stride]; draft is int32 [batch, k] (unused
+ * entries set to 0); draft_len is int32 [batch].  index_len (optional, int32
+ * [batch]) limits the candidates to p <= index_len[b] - 1: the positions a
+ * proposer has indexed so far (NgramProposer built on a prefix, not extended).
+ * max_n must be in [1, 8] and k in [0, 64].
+ */
+int oxr_ngram_propose(const int32_t* history, int64_t history_stride, const int32_t* history_len,
+                      const int32_t* index_len, int32_t batch, int32_t max_n, int32_t k, const int32_t* k_limit,
+                      int32_t* draft, int32_t* draft_len, oxr_stream_t stream);
+
+/*
+ * (1b) Drafting fused with verify-input assembly.
+ * Replaces Engine._speculate's draft loop and row assembly
+ * (oxr_runtime/engine.py:674-684, 700-710; slot_of at language.py:320-322):
+ * drafts as oxr_ngram_propose, then for row j < tokens_per_seq of sequence b
+ *   ids[b*S + j]       = j == 0 ? history[b, L-1] : (j-1 < draft_len ? draft[j-1] : 0)
+ *   positions[b*S + j] = seq_len[b] + j
+ *   slots[b*S + j]     = block_table[b, pos / block_size] * block_size + pos % block_size
+ *                        (-1 when pos / block_size >= table_stride)
+ *   attn_seq_lens[b]   = seq_len[b] + S
+ * seq_len is the KV length before the step (the reference's seq.length).
+ * tokens_per_seq (S) must be >= k + 1.  ids/positions/slots are int64 [B*S].
+ */
+int oxr_propose_verify_inputs(const int32_t* history, int64_t history_stride, const int32_t* history_len,
+                              int32_t batch, int32_t max_n, int32_t k, const int32_t* k_limit,
+                              const int32_t* seq_len, const int32_t* block_table, int64_t table_stride,
+                              int32_t block_size, int32_t tokens_per_seq, int32_t* draft, int32_t* draft_len,
+                              int64_t* ids, int64_t* positions, int64_t* slots, int32_t* attn_seq_lens,
+                              oxr_stream_t stream);
+
+/*
+ * (4c) Longest-prefix greedy acceptance + length rollback.
+ * Replaces speculative.accept (oxr_runtime/speculative.py:42-48) and the
+ * per-sequence bookkeeping of Engine._speculate/_take (engine.py:729-737,
+ * 647-664): a = longest prefix with draft[b, j] == predicted[b, j]
+ * (j < draft_len[b]); committed[b, :a+1] = predicted[b, :a+1] (rest -1);
+ * seq_len[b] += a + 1 (no KV data moves); the committed ids are appended to
+ * history[b] (history_len += appended) stopping at eos_id (not appended,
+ * finished = 1) or at max_tokens[b] (finished = 2).  Sequences with
+ * finished[b] != 0 on entry are left unchanged.  predicted is int64 [B, S]
+ * (the greedy ids of the verify step); committed is int32 [B, k+1].
+ * Optional (nullable): max_tokens, committed, num_committed, seq_len,
+ * history (+ history_len), finished.  eos_id < 0 disables the EOS stop.
+ */
+int oxr_accept(const int32_t* draft, const int32_t* draft_len, int32_t k, const int64_t* predicted,
+               int32_t tokens_per_seq, int32_t batch, int32_t eos_id, const int32_t* max_tokens, int32_t* accepted,
+               int32_t* committed, int32_t* num_committed, int32_t* seq_len, int32_t* history,
+               int64_t history_stride, int32_t* history_len, int32_t* finished, oxr_stream_t stream);
+
+/*
+ * (2) Fused q/k RMSNorm + NeoX RoPE + paged KV-cache write.
+ * Replaces kernels.qk_norm_rope_store / _launch (oxr_runtime/kernels.py:150-178):
+ * qkv bf16 [n, (H + 2*KV) * 128]; q_weight, k_weight bf16 [128]; cos, sin bf16
+ * [n, 64]; slots int64 [n]; k_cache, v_cache bf16 [num_slots, KV, 128] (the
+ * reference's [blocks, block_size, KV, 128] viewed flat).  Writes q_out bf16
+ * [n, H, 128] and, when k_out / v_out are non-null (need_kv=True), contiguous
+ * k_out / v_out bf16 [n, KV, 128].  num_slots = blocks * block_size; a slot
+ * outside [0, num_slots) is skipped instead of written out of bounds.  Rounding chain and the sum-of-squares
+ * addition tree follow kernels.py:79-111 and 181-213; rsqrt is 1/sqrt with
+ * both operations correctly rounded.  head_dim must be 128.
+ */
+int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                           const oxr_bf16* cos, const oxr_bf16* sin, float eps, oxr_bf16* k_cache,
+                           oxr_bf16* v_cache, const int64_t* slots, int64_t num_slots, int64_t n, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, oxr_bf16* q_out, oxr_bf16* k_out,
+                           oxr_bf16* v_out, oxr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OXR_VERIFY_H */

@@ -1,0 +1,104 @@
+"""ctypes binding of ``liboxr_verify.so``, the gfx950 C-ABI library (include/oxr_verify.h).
+
+torch is imported before the library is loaded so that the library binds to the
+HIP runtime torch already mapped (same SONAME), and stream handles and device
+pointers from torch are valid in both.  There is no CPU fallback: a missing
+library or a non-GPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("liboxr_verify.so")
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); kept in step with include/oxr_verify.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "oxr_abi_version": (ctypes.c_int, []),
+    "oxr_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "oxr_selftest_mfma_layout": (ctypes.c_int, [_P, _P, _P, _P]),
+    "oxr_ngram_propose": (ctypes.c_int, [_P, _I64, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "oxr_propose_verify_inputs": (
+        ctypes.c_int,
+        [_P, _I64, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
+    ),
+    "oxr_accept": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P]),
+    "oxr_qk_norm_rope_store": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _F32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class HipLibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the library, with argument types declared."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise HipLibraryMissing(
+                f"{LIB_PATH} is not built; run `python oxr-inference_amd/build.py` (hipcc, gfx950). "
+                "There is no CPU fallback."
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(status: int, name: str) -> None:
+    if status != 0:
+        message = lib().oxr_status_string(status).decode()
+        raise RuntimeError(f"{name} failed: {message} (status {status})")
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise on a non-zero status."""
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor, name: str) -> torch.device:
+    """All tensors on one GPU; raises for CPU tensors (there is no CPU path)."""
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"{name}: tensors must be on a GPU (got {t.device}); this build has no CPU path")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError(f"{name}: tensors on different devices ({device} and {t.device})")
+    if device is None:
+        raise RuntimeError(f"{name}: no tensor arguments")
+    return device
+
+
+def require(cond: bool, message: str) -> None:
+    if not cond:
+        raise ValueError(message)

@@ -1,0 +1,72 @@
+// Shared device helpers for the gfx950 verify-step kernels.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, MFMA
+// 16x16x32 bf16 tiles, 160 KB LDS per CU.  bf16 values travel as raw uint16_t
+// bits so that the C-ABI never exposes a compiler-specific bf16 type.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/oxr_verify.h"
+
+namespace oxr {
+
+typedef uint16_t bf16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32.  fp32 -> bf16 is round-to-nearest-even with NaN mapped to the
+// canonical quiet NaN 0x7FC0, the same convention torch's CPU BFloat16 uses.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Round an fp32 value to the nearest bf16 and return it widened back to fp32.
+__device__ __forceinline__ float round_bf16(float f) { return bf2f(f2bf(f)); }
+
+// Low / high bf16 of a packed pair.
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+__device__ __forceinline__ f32x4 mfma_16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+// 128-bit global loads/stores.  `nt` variants mark data that is streamed once
+// (weights, KV pages) so it does not evict reusable lines from L2.
+__device__ __forceinline__ u32x4 ld128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 ld128_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st128(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+}  // namespace oxr
+
+// Host-side helpers shared by the entry points.
+#define OXR_RETURN_IF(cond, code) \
+  do {                            \
+    if (cond) return (code);      \
+  } while (0)
+
+#define OXR_LAUNCH_STATUS() ((int)hipGetLastError())

@@ -1,0 +1,215 @@
+"""n-gram drafting and greedy acceptance on the GPU: the drop-in for oxr_runtime/speculative.py.
+
+The reference keeps a per-sequence Python dict (speculative.py:15-39) and accepts on the
+host after copying the verify step's greedy ids back (engine.py:727-733).  Here both run
+as gfx950 kernels over device-resident histories:
+
+- ``propose_batch``: all sequences' drafts in one launch (csrc/ngram.hip).
+- ``propose_verify_inputs``: drafting fused with the verify-row assembly of
+  engine.py:700-710 (ids, positions, slots, seq_lens), so the step needs no host data.
+- ``accept_batch``: longest-prefix acceptance, length rollback and history append for
+  all sequences in one launch (csrc/accept.hip).
+
+``NgramProposer`` and ``accept`` keep the reference's list-based signatures for callers
+that hold Python lists; they run the same kernels on a batch of one.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+
+_MAX_N = 4  # speculative.py:12
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("speculative: no GPU visible; this build has no CPU path")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _check_int32(name: str, t: torch.Tensor, dims: int) -> None:
+    _lib.require(t.dtype == torch.int32 and t.dim() == dims, f"{name} must be int32 with {dims} dims")
+    _lib.require(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def propose_batch(
+    history: torch.Tensor, history_len: torch.Tensor, k: int, *, max_n: int = _MAX_N,
+    k_limit: torch.Tensor | None = None, index_len: torch.Tensor | None = None,
+    draft: torch.Tensor | None = None, draft_len: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Drafts for every sequence: ``history`` int32 ``[B, capacity]`` with ``history_len[b]`` valid
+    tokens.  Returns (``draft`` int32 ``[B, k]`` zero-padded, ``draft_len`` int32 ``[B]``); row b is
+    ``NgramProposer(h).propose(h, min(k, k_limit[b]))`` of the reference for ``h = history[b, :len]``."""
+    device = _lib.require_gpu(history, history_len, k_limit, index_len, name="propose_batch")
+    _check_int32("history", history, 2)
+    _check_int32("history_len", history_len, 1)
+    b = history.shape[0]
+    _lib.require(history_len.shape[0] == b, "history_len must be [B]")
+    for name, t in (("k_limit", k_limit), ("index_len", index_len)):
+        if t is not None:
+            _check_int32(name, t, 1)
+            _lib.require(t.shape[0] == b, f"{name} must be [B]")
+    if draft is None:
+        draft = torch.empty(b, k, dtype=torch.int32, device=device)
+    if draft_len is None:
+        draft_len = torch.empty(b, dtype=torch.int32, device=device)
+    _lib.require(draft.shape == (b, k) and draft.dtype == torch.int32 and draft.is_contiguous(), "draft must be int32 [B, k]")
+    _check_int32("draft_len", draft_len, 1)
+    _lib.call(
+        "oxr_ngram_propose", history.data_ptr(), history.stride(0), history_len.data_ptr(), _lib.ptr(index_len), b,
+        max_n, k, _lib.ptr(k_limit), draft.data_ptr(), draft_len.data_ptr(), _lib.stream(device),
+    )
+    return draft, draft_len
+
+
+class VerifyInputs(NamedTuple):
+    draft: torch.Tensor          # int32 [B, k]
+    draft_len: torch.Tensor      # int32 [B]
+    ids: torch.Tensor            # int64 [B * S]
+    positions: torch.Tensor      # int64 [B * S]
+    slots: torch.Tensor          # int64 [B * S]
+    attn_seq_lens: torch.Tensor  # int32 [B]
+
+
+def alloc_verify_inputs(batch: int, k: int, tokens_per_seq: int, device: torch.device) -> VerifyInputs:
+    n = batch * tokens_per_seq
+    return VerifyInputs(
+        torch.zeros(batch, k, dtype=torch.int32, device=device), torch.zeros(batch, dtype=torch.int32, device=device),
+        torch.zeros(n, dtype=torch.int64, device=device), torch.zeros(n, dtype=torch.int64, device=device),
+        torch.zeros(n, dtype=torch.int64, device=device), torch.zeros(batch, dtype=torch.int32, device=device),
+    )
+
+
+def propose_verify_inputs(
+    history: torch.Tensor, history_len: torch.Tensor, k: int, seq_len: torch.Tensor, block_table: torch.Tensor,
+    block_size: int, tokens_per_seq: int, *, max_n: int = _MAX_N, k_limit: torch.Tensor | None = None,
+    out: VerifyInputs | None = None,
+) -> VerifyInputs:
+    """Drafting plus the verify rows of engine.py:700-710, all on the GPU.  ``seq_len`` is each
+    sequence's KV length before the step (the reference's ``seq.length``)."""
+    device = _lib.require_gpu(history, history_len, seq_len, block_table, k_limit, name="propose_verify_inputs")
+    _check_int32("history", history, 2)
+    _check_int32("history_len", history_len, 1)
+    _check_int32("seq_len", seq_len, 1)
+    _check_int32("block_table", block_table, 2)
+    b = history.shape[0]
+    _lib.require(tokens_per_seq >= k + 1, "tokens_per_seq must be at least k + 1")
+    _lib.require(block_table.shape[0] >= b and history_len.shape[0] == b and seq_len.shape[0] == b, "batch sizes differ")
+    if out is None:
+        out = alloc_verify_inputs(b, k, tokens_per_seq, device)
+    _lib.call(
+        "oxr_propose_verify_inputs", history.data_ptr(), history.stride(0), history_len.data_ptr(), b, max_n, k,
+        _lib.ptr(k_limit), seq_len.data_ptr(), block_table.data_ptr(), block_table.stride(0), block_size,
+        tokens_per_seq, out.draft.data_ptr(), out.draft_len.data_ptr(), out.ids.data_ptr(), out.positions.data_ptr(),
+        out.slots.data_ptr(), out.attn_seq_lens.data_ptr(), _lib.stream(device),
+    )
+    return out
+
+
+class AcceptResult(NamedTuple):
+    accepted: torch.Tensor       # int32 [B]: drafts accepted (a)
+    committed: torch.Tensor      # int32 [B, k+1]: predicted[:a+1], rest -1
+    num_committed: torch.Tensor  # int32 [B]: a + 1
+
+
+def accept_batch(
+    draft: torch.Tensor, draft_len: torch.Tensor, predicted: torch.Tensor, *, seq_len: torch.Tensor | None = None,
+    history: torch.Tensor | None = None, history_len: torch.Tensor | None = None, eos_id: int = -1,
+    max_tokens: torch.Tensor | None = None, finished: torch.Tensor | None = None, out: AcceptResult | None = None,
+) -> AcceptResult:
+    """speculative.accept for every sequence plus the engine's rollback (engine.py:729-737):
+    ``seq_len += a + 1`` and the committed ids appended to ``history`` (stopping at ``eos_id`` or
+    ``max_tokens``, reported in ``finished``).  ``predicted`` is the step's int64 ``[B, S]`` greedy ids."""
+    device = _lib.require_gpu(draft, draft_len, predicted, seq_len, history, history_len, max_tokens, finished,
+                              name="accept_batch")
+    _check_int32("draft", draft, 2)
+    _check_int32("draft_len", draft_len, 1)
+    b, k = draft.shape
+    _lib.require(predicted.dtype == torch.int64 and predicted.dim() == 2 and predicted.shape[0] == b
+                 and predicted.is_contiguous(), "predicted must be contiguous int64 [B, S]")
+    s = predicted.shape[1]
+    for name, t in (("seq_len", seq_len), ("history_len", history_len), ("max_tokens", max_tokens),
+                    ("finished", finished)):
+        if t is not None:
+            _check_int32(name, t, 1)
+            _lib.require(t.shape[0] == b, f"{name} must be [B]")
+    if history is not None:
+        _check_int32("history", history, 2)
+        _lib.require(history_len is not None, "history needs history_len")
+    if out is None:
+        out = AcceptResult(torch.empty(b, dtype=torch.int32, device=device),
+                           torch.empty(b, k + 1, dtype=torch.int32, device=device),
+                           torch.empty(b, dtype=torch.int32, device=device))
+    _lib.call(
+        "oxr_accept", draft.data_ptr(), draft_len.data_ptr(), k, predicted.data_ptr(), s, b, int(eos_id),
+        _lib.ptr(max_tokens), out.accepted.data_ptr(), out.committed.data_ptr(), out.num_committed.data_ptr(),
+        _lib.ptr(seq_len), _lib.ptr(history), history.stride(0) if history is not None else 0, _lib.ptr(history_len),
+        _lib.ptr(finished), _lib.stream(device),
+    )
+    return out
+
+
+class NgramProposer:
+    """speculative.py:15-39 with the same methods, over a device-resident copy of the history.
+
+    The history is mirrored on the GPU append-only: ``propose``/``extend`` upload only tokens
+    past the mirrored length (a shorter list re-uploads everything).  The index covers positions
+    up to the length at the last ``__init__``/``extend``, as the reference's dict does."""
+
+    def __init__(self, tokens: Sequence[int], *, max_n: int = _MAX_N):
+        self.max_n = max_n
+        self._device = _device()
+        self._buf = torch.zeros(max(64, 2 * len(tokens)), dtype=torch.int32, device=self._device)
+        self._mirrored = 0
+        self._indexed = len(tokens)
+        self._sync(tokens)
+
+    def _sync(self, tokens: Sequence[int]) -> None:
+        n = len(tokens)
+        if n < self._mirrored:
+            self._mirrored = 0
+        if n > self._buf.numel():
+            grown = torch.zeros(2 * n, dtype=torch.int32, device=self._device)
+            grown[: self._mirrored] = self._buf[: self._mirrored]
+            self._buf = grown
+        if n > self._mirrored:
+            new = torch.tensor(list(tokens[self._mirrored :]), dtype=torch.int32)
+            self._buf[self._mirrored : n].copy_(new)
+            self._mirrored = n
+
+    def extend(self, tokens: Sequence[int], old_length: int) -> None:
+        """``tokens`` from ``old_length`` on are new; index them (speculative.py:28-31)."""
+        self._sync(tokens)
+        self._indexed = max(self._indexed, len(tokens))
+
+    def propose(self, tokens: Sequence[int], k: int) -> list[int]:
+        """Up to ``k`` ids following the latest earlier occurrence of the longest matching suffix;
+        ``[]`` when nothing matches (speculative.py:33-39)."""
+        self._sync(tokens)
+        n = len(tokens)
+        hist = self._buf[:n].view(1, n) if n else self._buf[:1].view(1, 1)
+        length = torch.tensor([n], dtype=torch.int32, device=self._device)
+        index_len = torch.tensor([self._indexed], dtype=torch.int32, device=self._device)
+        draft, draft_len = propose_batch(hist, length, max(k, 0), max_n=self.max_n, index_len=index_len)
+        m = int(draft_len.item())
+        return draft[0, :m].tolist()
+
+
+def accept(draft: Sequence[int], predicted: Sequence[int]) -> list[int]:
+    """``predicted[j]`` is the model's choice after the previous token and ``draft[:j]``
+    (``len(predicted) == len(draft) + 1``).  Returns the matching prefix of ``draft`` plus the model's
+    next choice (speculative.py:42-48)."""
+    device = _device()
+    k = len(draft)
+    _lib.require(len(predicted) >= k + 1, "predicted must hold len(draft) + 1 ids")
+    d = torch.tensor([list(draft) or [0]], dtype=torch.int32).to(device)
+    dl = torch.tensor([k], dtype=torch.int32).to(device)
+    p = torch.tensor([list(predicted[: k + 1])], dtype=torch.int64).to(device)
+    res = accept_batch(d, dl, p)
+    a = int(res.accepted.item())
+    return list(draft[:a]) + [int(predicted[a])]

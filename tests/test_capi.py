@@ -1,0 +1,76 @@
+"""The C-ABI library loads on the CPU and exports exactly what include/oxr_verify.h declares,
+with the argument lists the ctypes binding uses.  No compute call is made here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from conftest import ROOT, pkg
+
+HEADER = ROOT / "include" / "oxr_verify.h"
+
+_CTYPE_OF = {
+    "int": ctypes.c_int, "int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+    "size_t": ctypes.c_size_t, "oxr_stream_t": ctypes.c_void_p, "void": None,
+}
+
+
+def _declarations() -> dict[str, list[str]]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[\w\s\*]+?\b(oxr_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        decls[m.group(1)] = args
+    return decls
+
+
+def _ctype(arg: str):
+    if "*" in arg:
+        return "char_p" if arg.startswith("const char") else ctypes.c_void_p
+    base = arg.replace("const ", "").split()[0]
+    return _CTYPE_OF[base]
+
+
+def test_header_declares_entry_points() -> None:
+    decls = _declarations()
+    for name in ("oxr_ngram_propose", "oxr_propose_verify_inputs", "oxr_qk_norm_rope_store", "oxr_accept"):
+        assert name in decls
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = pkg("_lib")
+    handle = ctypes.CDLL(str(lib.LIB_PATH))
+    for name in _declarations():
+        assert hasattr(handle, name), f"{name} declared in {HEADER.name} but not exported"
+
+
+def test_ctypes_signatures_match_header() -> None:
+    lib = pkg("_lib")
+    decls = _declarations()
+    assert set(lib.SIGNATURES) == set(decls)
+    for name, args in decls.items():
+        _, argtypes = lib.SIGNATURES[name]
+        assert len(argtypes) == len(args), name
+        for arg, bound in zip(args, argtypes):
+            want = _ctype(arg)
+            if want == "char_p":
+                continue
+            assert bound == want, (name, arg, bound)
+
+
+def test_status_strings_and_version() -> None:
+    lib = pkg("_lib").lib()
+    assert lib.oxr_abi_version() == 1
+    assert b"unsupported" in lib.oxr_status_string(-2)
+    assert lib.oxr_status_string(0) == b"ok"
+
+
+def test_entry_points_reject_bad_arguments_before_launch() -> None:
+    """Validation happens on the host: invalid sizes return an error code and launch nothing."""
+    lib = pkg("_lib").lib()
+    assert lib.oxr_qk_norm_rope_store(None, None, None, None, None, 1e-6, None, None, None, 0, 4, 16, 8, 64,
+                                      None, None, None, None) == -2  # head_dim != 128
+    assert lib.oxr_ngram_propose(None, 0, None, None, 1, 9, 3, None, None, None, None) == -2  # max_n > 8
+    assert lib.oxr_ngram_propose(None, 0, None, None, 0, 4, 3, None, None, None, None) == 0  # empty batch

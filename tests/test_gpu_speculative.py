@@ -1,0 +1,197 @@
+"""gfx950 drafting, verify-input assembly and acceptance vs the oracle (bit-exact, integer).
+
+Covers the reference's known answers (tests/test_speculative.py:8-41) through the list
+API, workload-1 histories, random small-vocabulary histories for every n cap, prefix
+indexing, k limits, empty and length-1 histories, 16k-token histories, and the engine's
+row assembly (engine.py:700-710) and bookkeeping (engine.py:729-737, 647-664).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, pkg
+from oracle import ngram
+
+pytestmark = pytest.mark.gpu
+spec = pkg("speculative")
+workloads = pkg("workloads")
+
+
+def _gpu_drafts(rows: list[list[int]], k: int, max_n: int, k_limit=None, index_len=None):
+    cap = max(1, max((len(r) for r in rows), default=1))
+    hist = np.zeros((len(rows), cap), dtype=np.int32)
+    for i, r in enumerate(rows):
+        hist[i, : len(r)] = r
+    lens = torch.tensor([len(r) for r in rows], dtype=torch.int32, device="cuda")
+    kl = None if k_limit is None else torch.tensor(k_limit, dtype=torch.int32, device="cuda")
+    il = None if index_len is None else torch.tensor(index_len, dtype=torch.int32, device="cuda")
+    draft, dlen = spec.propose_batch(torch.from_numpy(hist).cuda(), lens, k, max_n=max_n, k_limit=kl, index_len=il)
+    draft, dlen = draft.cpu().numpy(), dlen.cpu().numpy()
+    return [draft[i, : dlen[i]].tolist() for i in range(len(rows))], draft, dlen
+
+
+def test_list_api_known_answers() -> None:
+    announce("known answers")
+    td, end, one, two = 10, 11, 1, 2
+    tokens = [td, one, end, td, two, end, td]
+    assert spec.NgramProposer(tokens).propose(tokens, 3) == [two, end, td]
+    assert spec.NgramProposer([1, 2, 3, 4]).propose([1, 2, 3, 4], 8) == []
+    tokens = [5, 6, 7, 5, 6, 8, 5, 6, 7, 9, 5, 6]
+    incremental = spec.NgramProposer(tokens[:5])
+    incremental.extend(tokens, 5)
+    for k in (1, 2, 4):
+        assert incremental.propose(tokens, k) == ngram.NgramIndex(tokens).propose(tokens, k)
+    assert spec.accept([7, 8, 9, 10], [7, 8, 3, 0, 0]) == [7, 8, 3]
+    assert spec.accept([7, 8], [7, 8, 5]) == [7, 8, 5]
+    assert spec.accept([7, 8], [1, 8, 5]) == [1]
+    assert spec.accept([], [4]) == [4]
+
+
+def test_stale_index_matches_reference_dict() -> None:
+    """A proposer built on a prefix and not extended only knows the prefix's positions."""
+    rng = np.random.default_rng(5)
+    announce("stale index")
+    for _ in range(20):
+        tokens = rng.integers(0, 4, size=int(rng.integers(2, 40))).tolist()
+        prefix = int(rng.integers(0, len(tokens) + 1))
+        want = ngram.NgramIndex(tokens[:prefix]).propose(tokens, 3)
+        assert spec.NgramProposer(tokens[:prefix]).propose(tokens, 3) == want
+
+
+@pytest.mark.parametrize("max_n", [1, 2, 3, 4, 8])
+def test_random_small_vocab_histories(max_n: int) -> None:
+    rng = np.random.default_rng(100 + max_n)
+    rows = [rng.integers(0, int(rng.integers(2, 6)), size=int(rng.integers(0, 700))).tolist() for _ in range(64)]
+    ks = [0, 1, 3, 8]
+    announce("random histories", max_n)
+    for k in ks:
+        got, _, _ = _gpu_drafts(rows, k, max_n)
+        want = [ngram.propose_closed_form(r, k, max_n) for r in rows]
+        assert got == want
+
+
+def test_prefix_index_and_k_limit() -> None:
+    rng = np.random.default_rng(7)
+    rows = [rng.integers(0, 3, size=int(rng.integers(1, 300))).tolist() for _ in range(32)]
+    index_len = [int(rng.integers(0, len(r) + 1)) for r in rows]
+    k_limit = [int(x) for x in rng.integers(-2, 6, size=len(rows))]
+    announce("prefix index + k_limit")
+    got, draft, _ = _gpu_drafts(rows, 4, 4, k_limit=k_limit, index_len=index_len)
+    for i, r in enumerate(rows):
+        kb = max(0, min(4, k_limit[i]))
+        assert got[i] == ngram.NgramIndex(r[: index_len[i]]).propose(r, kb)
+        assert (draft[i, len(got[i]) :] == 0).all()
+
+
+def test_edge_histories() -> None:
+    rows = [[], [7], [7, 7], [3, 3, 3, 3, 3], [1, 2, 3], [9, 1, 9], list(range(300)) + [0]]
+    announce("edge histories")
+    for max_n in (1, 4):
+        got, _, _ = _gpu_drafts(rows, 3, max_n)
+        assert got == [ngram.NgramIndex(r, max_n).propose(r, 3) for r in rows]
+
+
+def test_workload1_histories_all_caps() -> None:
+    histories = workloads.drafting_histories(seed=0)
+    rows = [h.tolist() for h in histories]
+    announce("workload1")
+    for max_n in (3, 4):
+        got, _, dlen = _gpu_drafts(rows, 3, max_n)
+        assert got == [ngram.NgramIndex(r, max_n).propose(r, 3) for r in rows]
+        assert dlen[0] == 3 and dlen[-1] == 0
+
+
+def test_long_histories() -> None:
+    """16k-token histories: matches far from the end, near the start, and none."""
+    rng = np.random.default_rng(9)
+    L = 16384
+    base = rng.permutation(workloads.VOCAB)[:L].astype(np.int32)
+    far = base.copy()
+    far[100:104] = far[-4:]  # only match is near the start
+    near = workloads.repetitive_history(rng, L, repetitive_tail=True)
+    rows = [base.tolist(), far.tolist(), near.tolist()]
+    announce("long histories")
+    got, _, _ = _gpu_drafts(rows, 3, 4)
+    assert got == [ngram.propose_closed_form(r, 3, 4) for r in rows]
+    assert got[1] == far[104:107].tolist()
+
+
+def test_verify_inputs_assembly() -> None:
+    rng = np.random.default_rng(11)
+    B, k, S, bs = 8, 3, 4, 16
+    histories = [workloads.repetitive_history(rng, int(rng.integers(50, 400)), repetitive_tail=bool(i % 2))
+                 for i in range(B)]
+    cap = 512
+    hist = np.zeros((B, cap), dtype=np.int32)
+    for i, h in enumerate(histories):
+        hist[i, : len(h)] = h
+    seq_len = rng.integers(100, 1000, size=B).astype(np.int32)
+    width = 80
+    table = rng.permutation(4096)[: B * width].reshape(B, width).astype(np.int32)
+    announce("verify inputs")
+    out = spec.propose_verify_inputs(
+        torch.from_numpy(hist).cuda(), torch.tensor([len(h) for h in histories], dtype=torch.int32, device="cuda"), k,
+        torch.from_numpy(seq_len).cuda(), torch.from_numpy(table).cuda(), bs, S, max_n=4,
+    )
+    ids, pos, slots = out.ids.cpu().numpy(), out.positions.cpu().numpy(), out.slots.cpu().numpy()
+    for b, h in enumerate(histories):
+        tokens = h.tolist()
+        draft = ngram.NgramIndex(tokens).propose(tokens, k)
+        row = [tokens[-1], *draft] + [0] * (S - 1 - len(draft))  # engine.py:703-709
+        assert ids[b * S : (b + 1) * S].tolist() == row
+        for j in range(S):
+            p = int(seq_len[b]) + j
+            assert pos[b * S + j] == p
+            assert slots[b * S + j] == table[b, p // bs] * bs + p % bs  # language.py:320-322
+    assert out.attn_seq_lens.cpu().numpy().tolist() == (seq_len + S).tolist()
+
+
+def test_accept_batch_and_rollback() -> None:
+    rng = np.random.default_rng(13)
+    B, k, S = 64, 3, 4
+    draft = rng.integers(0, 5, size=(B, k)).astype(np.int32)
+    dlen = rng.integers(0, k + 1, size=B).astype(np.int32)
+    for b in range(B):
+        draft[b, dlen[b] :] = 0
+    predicted = rng.integers(0, 5, size=(B, S)).astype(np.int64)
+    predicted[::3, :k] = draft[::3]  # some full accepts
+    seq_len = rng.integers(10, 100, size=B).astype(np.int32)
+    cap = 64
+    hist_len = rng.integers(1, 50, size=B).astype(np.int32)
+    hist = rng.integers(0, 5, size=(B, cap)).astype(np.int32)
+    eos = 4
+    max_tokens = rng.integers(2, 60, size=B).astype(np.int32)
+    d = lambda a: torch.from_numpy(a).cuda()
+    seq_t, hist_t, hlen_t, fin_t = d(seq_len.copy()), d(hist.copy()), d(hist_len.copy()), torch.zeros(B, dtype=torch.int32, device="cuda")
+    announce("accept batch")
+    res = spec.accept_batch(d(draft), d(dlen), d(predicted), seq_len=seq_t, history=hist_t, history_len=hlen_t,
+                            eos_id=eos, max_tokens=d(max_tokens), finished=fin_t)
+    acc, com = res.accepted.cpu().numpy(), res.committed.cpu().numpy()
+    for b in range(B):
+        taken = ngram.accept(draft[b, : dlen[b]].tolist(), predicted[b, : dlen[b] + 1].tolist())
+        a = len(taken) - 1
+        assert acc[b] == a and com[b, : a + 1].tolist() == taken and (com[b, a + 1 :] == -1).all()
+        assert seq_t[b].item() == seq_len[b] + a + 1
+        # engine.py:647-664: EOS finishes without appending; max_tokens finishes after appending.
+        out = hist[b, : hist_len[b]].tolist()
+        reason = 0
+        for t in taken:
+            if t == eos:
+                reason = 1
+                break
+            out.append(t)
+            if len(out) >= max_tokens[b]:
+                reason = 2
+                break
+        assert hlen_t[b].item() == len(out) and hist_t[b, : len(out)].cpu().tolist() == out
+        assert fin_t[b].item() == reason
+    # Finished sequences take nothing on the next call.
+    before = seq_t.clone()
+    done = fin_t.cpu().numpy() != 0
+    assert done.any() and not done.all()
+    spec.accept_batch(d(draft), d(dlen), d(predicted), seq_len=seq_t, history=hist_t, history_len=hlen_t,
+                      eos_id=eos, max_tokens=d(max_tokens), finished=fin_t)
+    assert np.array_equal(seq_t.cpu().numpy()[done], before.cpu().numpy()[done])
