@@ -117,6 +117,28 @@ int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_weight, const 
                            int32_t num_kv_heads, int32_t head_dim, oxr_bf16* q_out, oxr_bf16* k_out,
                            oxr_bf16* v_out, oxr_stream_t stream);
 
+/*
+ * (3) Multi-query causal paged attention of the verify step.
+ * Replaces attention.paged_extend (oxr_runtime/attention.py:96-109); math as
+ * the reference test stub (tests/test_language_fused.py:19-28, 50-57):
+ * q bf16 [B, S, H, 128]; k_cache, v_cache bf16 [num_blocks, block_size, KV,
+ * 128]; seq_lens int32 [B] (including the S new tokens, whose K/V are already
+ * in the cache); block_table int32 [B, table_stride].  Token s of sequence b
+ * attends keys [0, seq_lens[b] - S + s] of kv head h / (H / KV) with scores
+ * q.k * scale and an fp32 softmax; out bf16 [B, S, H, 128].
+ * Requires H % KV == 0, S * (H / KV) <= 16, block_size a power of two,
+ * max_seq_len <= table_stride * block_size; contexts longer than max_seq_len
+ * are clamped to it.  workspace: at least
+ * oxr_paged_extend_workspace_bytes(batch, KV, max_seq_len) bytes of device
+ * memory (partials of the context split; no initial contents needed).
+ */
+size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
+int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache, const int32_t* seq_lens,
+                     const int32_t* block_table, int64_t table_stride, int32_t batch, int32_t tokens_per_seq,
+                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out, void* workspace,
+                     size_t workspace_bytes, oxr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

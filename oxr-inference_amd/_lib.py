@@ -32,6 +32,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _I64, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
     ),
     "oxr_accept": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P]),
+    "oxr_paged_extend_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _I32]),
+    "oxr_paged_extend": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I32, _F32, _P, _P, _SZ, _P],
+    ),
     "oxr_qk_norm_rope_store": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _F32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _P],

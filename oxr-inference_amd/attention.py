@@ -1,0 +1,59 @@
+"""Multi-query causal paged attention: the drop-in for attention.paged_extend (oxr_runtime/attention.py:96-109).
+
+Runs the gfx950 kernels of csrc/paged_attention.hip (MFMA QK^T and PV tiles, context split
+across single-wave workgroups, log-sum-exp merge).  Only the verify-step entry point is
+provided; the reference's prefill/vision/decode entry points (``varlen``,
+``varlen_bidirectional``, ``paged_decode``, ``rotary``) are outside this build.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def workspace_bytes(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
+    return int(_lib.lib().oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len))
+
+
+def paged_extend(
+    q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
+    block_table: torch.Tensor, *, scale: float | None = None, max_seq_len: int | None = None,
+    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Each sequence brings S new tokens (``q`` is ``[B, S, heads, dim]``; their K/V are already in the
+    paged cache); token j sees itself and everything before it (``seq_lens`` includes the S tokens).
+    Returns ``[B, S, heads, dim]``.
+
+    ``max_seq_len`` bounds every ``seq_lens[b]`` (default: the block table's span) and sizes the
+    context split; ``out`` and ``workspace`` (bytes from :func:`workspace_bytes`) may be passed in
+    to avoid allocations."""
+    device = _lib.require_gpu(q, k_cache, v_cache, seq_lens, block_table, name="paged_extend")
+    _lib.require(q.dim() == 4 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [B, S, H, D]")
+    b, s, h, d = q.shape
+    _lib.require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "caches must be [blocks, block_size, KV, D]")
+    _lib.require(k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16, "caches must be bf16")
+    _lib.require(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    num_blocks, block_size, kv, dk = k_cache.shape
+    _lib.require(dk == d, "head_dim of q and caches differ")
+    _lib.require(seq_lens.dtype == torch.int32 and seq_lens.shape == (b,), "seq_lens must be int32 [B]")
+    _lib.require(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] >= b,
+                 "block_table must be int32 [>=B, W]")
+    _lib.require(block_table.stride(1) == 1, "block_table rows must be contiguous")
+    if max_seq_len is None:
+        max_seq_len = block_table.shape[1] * block_size
+    if scale is None:
+        scale = d ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    need = workspace_bytes(b, kv, max_seq_len)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    _lib.call(
+        "oxr_paged_extend", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), seq_lens.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), b, s, h, kv, d, block_size, num_blocks, max_seq_len,
+        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _lib.stream(device),
+    )
+    return out

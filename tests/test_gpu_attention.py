@@ -1,0 +1,88 @@
+"""gfx950 paged verify attention vs the oracle (bf16 tolerance: |err| <= 2e-2 + 1e-2 |ref|).
+
+Config 3 of the benchmark (B=8, S=4, 16/8 heads, contexts U{2048..8192}, block 16, block
+tables from a permutation of a 65,536-block pool), plus ragged and edge shapes: contexts
+shorter than one 32-key step, not multiples of the block or chunk size, block size 256
+(the reference's), one kv head per q head, and S=1.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, pkg
+from oracle import attention as oracle_attention
+
+pytestmark = pytest.mark.gpu
+attention = pkg("attention")
+workloads = pkg("workloads")
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _run(seq_lens, S, H, KV, block_size, num_blocks, seed, table_width=None, max_seq_len=None):
+    rng = np.random.default_rng(seed)
+    B = len(seq_lens)
+    seq_lens = np.asarray(seq_lens, dtype=np.int32)
+    need = (seq_lens + block_size - 1) // block_size
+    width = table_width or int(need.max())
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    table = np.full((B, width), -7, dtype=np.int32)  # unused entries are garbage on purpose
+    off = 0
+    for b in range(B):
+        table[b, : need[b]] = perm[off : off + need[b]]
+        off += need[b]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    vc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn(B, S, H, 128, generator=g, device="cuda").to(torch.bfloat16)
+    table_t = torch.from_numpy(table).cuda()
+    out = attention.paged_extend(q, kc, vc, torch.from_numpy(seq_lens).cuda(), table_t, max_seq_len=max_seq_len)
+    torch.cuda.synchronize()
+    k_rows, v_rows = [], []
+    for b in range(B):
+        blocks = torch.from_numpy(table[b, : need[b]].astype(np.int64)).cuda()
+        k_rows.append(_bits(kc[blocks].flatten(0, 1)[: seq_lens[b]]))
+        v_rows.append(_bits(vc[blocks].flatten(0, 1)[: seq_lens[b]]))
+    exact, _ = oracle_attention.paged_extend(_bits(q), k_rows, v_rows, 128 ** -0.5)
+    got = out.float().cpu().numpy()
+    err = np.abs(got - exact)
+    bound = ATOL + RTOL * np.abs(exact)
+    assert (err <= bound).all(), f"max err {err.max():.3g}, worst excess {(err - bound).max():.3g}"
+    return err.max()
+
+
+def test_config3_bit_budget() -> None:
+    rng = np.random.default_rng(30)
+    seq_lens = rng.integers(2048, 8193, size=8)
+    announce("attention config3", seq_lens.tolist())
+    err = _run(seq_lens, 4, 16, 8, 16, 65_536, seed=31)
+    print("max abs err", err)
+
+
+@pytest.mark.parametrize("seq_lens", [[4, 5, 17, 31], [32, 33, 255, 256, 257, 300], [1000, 4097, 511, 7]])
+def test_ragged_contexts(seq_lens) -> None:
+    announce("attention ragged", seq_lens)
+    _run(seq_lens, 4, 16, 8, 16, 4096, seed=32)
+
+
+def test_reference_block_size_256_and_table_slack() -> None:
+    announce("attention block 256")
+    _run([300, 700, 40], 4, 16, 8, 256, 64, seed=33, table_width=8)
+
+
+def test_single_token_and_mha() -> None:
+    announce("attention S=1, H=KV")
+    _run([100, 1, 65], 1, 8, 8, 16, 256, seed=34)
+    _run([70, 90], 2, 8, 8, 16, 256, seed=35)
+
+
+def test_max_seq_len_bounds_chunks() -> None:
+    announce("attention max_seq_len")
+    _run([600, 1200], 4, 16, 8, 16, 1024, seed=36, table_width=200, max_seq_len=1300)
