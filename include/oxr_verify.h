@@ -139,6 +139,42 @@ int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16*
                      int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out, void* workspace,
                      size_t workspace_bytes, oxr_stream_t stream);
 
+/*
+ * (4a) Weight-streaming bf16 GEMM Y = X * W^T with a fused epilogue.
+ * Replaces the nn.Linear projections of the verify forward (language.py:261
+ * qkv_proj, 268 o_proj, 269 gate_up_proj/down_proj) together with the
+ * elementwise op that follows each:
+ *   OXR_EPI_STORE        y = bf16(x @ w^T)                          y [m, n]
+ *   OXR_EPI_SILU_MUL     w holds 2n rows (gate then up, language.py:238);
+ *                        y = bf16(bf16(silu(bf16(g))) * bf16(u))      y [m, n]
+ *                        (_silu_mul, language.py:102-104)
+ *   OXR_EPI_ADD_RESIDUAL y = bf16(bf16(x @ w^T) + y), in place: the residual
+ *                        add of _add_rms_norm (language.py:94-99)
+ * x bf16 [m, ldx] (first k columns used), w bf16 [rows, k] row-major, fp32
+ * accumulation.  m <= 64, k a multiple of 128, x and w 16-byte aligned.
+ */
+#define OXR_EPI_STORE 0
+#define OXR_EPI_SILU_MUL 1
+#define OXR_EPI_ADD_RESIDUAL 3
+int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
+                  int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream);
+
+/*
+ * (4b) LM head GEMM with fused vocab-wide argmax.
+ * Replaces LanguageModel.logits (language.py:213-214) followed by
+ * argmax(dim=-1) (decode_graph.py:167, engine.py:726): logits = hidden @
+ * weight^T in fp32, rounded to bf16, and predicted[i] = the first index of
+ * the largest bf16 logit of row i (NaN counts as largest, -0 == +0).
+ * hidden bf16 [m, hidden_size]; weight bf16 [vocab, hidden_size]; predicted
+ * int64 [m].  logits (optional, bf16 [m, vocab]) receives the bf16 logits.
+ * m <= 64; hidden_size a multiple of 128.  workspace: at least
+ * oxr_lm_head_workspace_bytes(m, vocab) bytes (per-tile maxima).
+ */
+size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab);
+int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
+                       oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes,
+                       oxr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,52 @@
+"""LM head with fused vocab-wide argmax (csrc/gemm.hip), replacing ``LanguageModel.logits``
+(language.py:213-214) followed by ``argmax(dim=-1)`` (decode_graph.py:167, engine.py:726).
+
+The logits are computed tile by tile in fp32, rounded to bf16 (as the reference's bf16
+``nn.Linear`` output) and reduced to the first index of the largest value without writing
+them out, unless the caller asks for them."""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+MAX_ROWS = 64
+
+
+def workspace_bytes(rows: int, vocab: int) -> int:
+    return int(_lib.lib().oxr_lm_head_workspace_bytes(min(rows, MAX_ROWS), vocab))
+
+
+def lm_head_argmax(
+    hidden: torch.Tensor, weight: torch.Tensor, *, return_logits: bool = False, predicted: torch.Tensor | None = None,
+    logits: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """hidden bf16 ``[n, hidden]``, weight bf16 ``[vocab, hidden]`` -> (int64 ``[n]`` greedy ids,
+    bf16 ``[n, vocab]`` logits when ``return_logits`` else None)."""
+    device = _lib.require_gpu(hidden, weight, name="lm_head_argmax")
+    _lib.require(hidden.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "bf16 operands required")
+    _lib.require(hidden.dim() == 2 and weight.dim() == 2 and hidden.shape[1] == weight.shape[1], "shape mismatch")
+    _lib.require(hidden.stride(1) == 1 and weight.is_contiguous(), "rows must be contiguous")
+    n, k = hidden.shape
+    vocab = weight.shape[0]
+    if predicted is None:
+        predicted = torch.empty(n, dtype=torch.int64, device=device)
+    if return_logits and logits is None:
+        logits = torch.empty(n, vocab, dtype=torch.bfloat16, device=device)
+    need = workspace_bytes(n, vocab)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    for start in range(0, n, MAX_ROWS):
+        rows = min(MAX_ROWS, n - start)
+        _lib.call(
+            "oxr_lm_head_argmax", hidden[start:].data_ptr(), rows, weight.data_ptr(), k, vocab,
+            logits[start:].data_ptr() if logits is not None else None, predicted[start:].data_ptr(),
+            workspace.data_ptr(), workspace.numel(), _lib.stream(device),
+        )
+    return predicted, logits
+
+
+def logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``LanguageModel.logits``: bf16 ``hidden @ weight.T`` (language.py:213-214)."""
+    return lm_head_argmax(hidden, weight, return_logits=True)[1]
