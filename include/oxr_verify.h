@@ -118,6 +118,37 @@ int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_weight, const 
                            oxr_bf16* v_out, oxr_stream_t stream);
 
 /*
+ * (2b) The same kernel reading cos/sin straight from the model's RoPE tables:
+ * row positions[i] of cos_table / sin_table (bf16 [table_rows, 64]), i.e. the
+ * gather rope_cos[positions] of LanguageModel.extend (language.py:204) fused
+ * into the kernel.  Positions outside the table are clamped to it.
+ */
+int oxr_qk_norm_rope_store_at(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                              const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,
+                              const int64_t* positions, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache,
+                              const int64_t* slots, int64_t num_slots, int64_t n, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_dim, oxr_bf16* q_out, oxr_bf16* k_out,
+                              oxr_bf16* v_out, oxr_stream_t stream);
+
+/*
+ * RMSNorm of rows (language.py:69-72): out = bf16(w * bf16(x * 1/sqrt(mean(x^2) + eps))),
+ * fp32 statistics.  x bf16 [rows, ldx]; hidden a multiple of 512 up to 4096.
+ * Used for the decoder norms after the residual add has been fused into the
+ * preceding GEMM (OXR_EPI_ADD_RESIDUAL).
+ */
+int oxr_rms_norm(const oxr_bf16* x, int64_t ldx, int64_t rows, int64_t hidden, const oxr_bf16* weight, float eps,
+                 oxr_bf16* out, int64_t ldo, oxr_stream_t stream);
+
+/*
+ * Embedding gather + first RMSNorm of the verify forward: residual[i] =
+ * table[ids[i]] (decode_graph.py:164 embed_tokens(ids)), out[i] =
+ * rms_norm(residual[i]) (language.py:253-255, layer 0's input norm).  Ids
+ * outside [0, vocab) are clamped.  residual and out are bf16 [rows, hidden].
+ */
+int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, int64_t vocab, int64_t hidden,
+                       const oxr_bf16* weight, float eps, oxr_bf16* residual, oxr_bf16* out, oxr_stream_t stream);
+
+/*
  * (3) Multi-query causal paged attention of the verify step.
  * Replaces attention.paged_extend (oxr_runtime/attention.py:96-109); math as
  * the reference test stub (tests/test_language_fused.py:19-28, 50-57):

@@ -37,6 +37,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I32, _F32, _P, _P, _SZ, _P],
     ),
+    "oxr_qk_norm_rope_store_at": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _I64, _P, _F32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
+    ),
+    "oxr_rms_norm": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _F32, _P, _I64, _P]),
+    "oxr_embed_rms_norm": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _F32, _P, _P, _P]),
     "oxr_gemm_bf16": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I64, _P]),
     "oxr_lm_head_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "oxr_lm_head_argmax": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),

@@ -51,7 +51,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(
     const bf16_t* __restrict__ cos_table, const bf16_t* __restrict__ sin_table, float eps,
     bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache, const int64_t* __restrict__ slots,
     int64_t num_slots, int64_t total_heads, int num_heads, int num_kv_heads, bf16_t* __restrict__ q_out,
-    bf16_t* __restrict__ k_out, bf16_t* __restrict__ v_out) {
+    bf16_t* __restrict__ k_out, bf16_t* __restrict__ v_out, const int64_t* __restrict__ positions,
+    int64_t table_rows) {
   const int heads_per_token = num_heads + 2 * num_kv_heads;
   int64_t g = (int64_t)blockIdx.x * kHeadsPerBlock + threadIdx.x / kLanesPerHead;
   const int s = threadIdx.x % kLanesPerHead;
@@ -94,8 +95,15 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(
   // which lives in lane s ^ 8 at the same register position.
   float c[8], sn[8], out[8];
   const int j0 = (s & 7) * 8;
-  unpack8(ld128(cos_table + t * (kHeadDim / 2) + j0), c);
-  unpack8(ld128(sin_table + t * (kHeadDim / 2) + j0), sn);
+  // cos/sin row: the token's own row, or the table row of its position
+  // (rope_cos[positions], language.py:204) when positions are given.
+  int64_t trow = t;
+  if (positions) {
+    trow = positions[t];
+    trow = trow < 0 ? 0 : (trow >= table_rows ? table_rows - 1 : trow);
+  }
+  unpack8(ld128(cos_table + trow * (kHeadDim / 2) + j0), c);
+  unpack8(ld128(sin_table + trow * (kHeadDim / 2) + j0), sn);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float other = shfl_xor_f(y[e], 8);
@@ -122,12 +130,13 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(
 }  // namespace
 }  // namespace oxr
 
-extern "C" int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
-                                      const oxr_bf16* cos, const oxr_bf16* sin, float eps, oxr_bf16* k_cache,
-                                      oxr_bf16* v_cache, const int64_t* slots, int64_t num_slots, int64_t n,
-                                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, oxr_bf16* q_out,
-                                      oxr_bf16* k_out, oxr_bf16* v_out, oxr_stream_t stream) {
-  using namespace oxr;
+namespace oxr {
+namespace {
+int launch_qk(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight, const oxr_bf16* cos,
+              const oxr_bf16* sin, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache, const int64_t* slots,
+              int64_t num_slots, int64_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+              oxr_bf16* q_out, oxr_bf16* k_out, oxr_bf16* v_out, const int64_t* positions, int64_t table_rows,
+              oxr_stream_t stream) {
   OXR_RETURN_IF(n < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_slots < 0, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(head_dim != kHeadDim, OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF((k_out == nullptr) != (v_out == nullptr), OXR_ERR_INVALID_ARG);
@@ -141,11 +150,33 @@ extern "C" int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_wei
   if (k_out) {
     hipLaunchKernelGGL(qk_norm_rope_store_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, qkv, q_weight,
                        k_weight, cos, sin, eps, k_cache, v_cache, slots, num_slots, total, num_heads, num_kv_heads,
-                       q_out, k_out, v_out);
+                       q_out, k_out, v_out, positions, table_rows);
   } else {
     hipLaunchKernelGGL(qk_norm_rope_store_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, qkv,
                        q_weight, k_weight, cos, sin, eps, k_cache, v_cache, slots, num_slots, total, num_heads,
-                       num_kv_heads, q_out, nullptr, nullptr);
+                       num_kv_heads, q_out, nullptr, nullptr, positions, table_rows);
   }
   return OXR_LAUNCH_STATUS();
+}
+}  // namespace
+}  // namespace oxr
+
+extern "C" int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                                      const oxr_bf16* cos, const oxr_bf16* sin, float eps, oxr_bf16* k_cache,
+                                      oxr_bf16* v_cache, const int64_t* slots, int64_t num_slots, int64_t n,
+                                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, oxr_bf16* q_out,
+                                      oxr_bf16* k_out, oxr_bf16* v_out, oxr_stream_t stream) {
+  return oxr::launch_qk(qkv, q_weight, k_weight, cos, sin, eps, k_cache, v_cache, slots, num_slots, n, num_heads,
+                        num_kv_heads, head_dim, q_out, k_out, v_out, nullptr, 0, stream);
+}
+
+extern "C" int oxr_qk_norm_rope_store_at(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                                         const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,
+                                         const int64_t* positions, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache,
+                                         const int64_t* slots, int64_t num_slots, int64_t n, int32_t num_heads,
+                                         int32_t num_kv_heads, int32_t head_dim, oxr_bf16* q_out, oxr_bf16* k_out,
+                                         oxr_bf16* v_out, oxr_stream_t stream) {
+  if (n > 0 && (!positions || table_rows <= 0)) return OXR_ERR_INVALID_ARG;
+  return oxr::launch_qk(qkv, q_weight, k_weight, cos_table, sin_table, eps, k_cache, v_cache, slots, num_slots, n,
+                        num_heads, num_kv_heads, head_dim, q_out, k_out, v_out, positions, table_rows, stream);
 }

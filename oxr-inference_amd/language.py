@@ -1,0 +1,263 @@
+"""Qwen3-style decoder verify forward on gfx950 kernels: the drop-in for the verify half of
+oxr_runtime/language.py (``LanguageModel.extend`` + ``logits``, language.py:149-214, 247-317).
+
+Per layer (language.py:301-317 with the fused projections of :234-245):
+
+    h        = rms_norm(residual)                               oxr_rms_norm / oxr_embed_rms_norm
+    qkv      = h @ Wqkv^T                                       oxr_gemm_bf16
+    q        = qk_norm_rope_store(qkv, ...)  (K/V -> cache)     oxr_qk_norm_rope_store_at
+    attn     = paged_extend(q, cache, seq_lens, block_table)    oxr_paged_extend
+    residual = bf16(bf16(attn @ Wo^T) + residual)               oxr_gemm_bf16 (add epilogue)
+    h        = rms_norm(residual)                               oxr_rms_norm
+    act      = silu(h @ Wg^T) * (h @ Wu^T)                      oxr_gemm_bf16 (SiLU*mul epilogue)
+    residual = bf16(bf16(act @ Wd^T) + residual)                oxr_gemm_bf16 (add epilogue)
+
+then ``hidden = rms_norm(residual)`` and the LM head with fused argmax.  The residual adds of
+``_add_rms_norm`` (language.py:94-99) move into the GEMM epilogues; the rounding points are
+the reference's (residual stored in bf16 before it is normalised).
+
+All intermediate buffers live in a preallocated :class:`StepBuffers`, so a forward enqueues
+kernels only and can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib, attention, gemm, lm_head
+from .kv_cache import KVCache
+
+
+@dataclass(frozen=True)
+class LanguageConfig:
+    """The shapes language.py reads from config.json (config.py:38-50)."""
+
+    hidden_size: int
+    intermediate_size: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    rms_norm_eps: float
+    rope_theta: float
+    vocab_size: int
+
+    @property
+    def qkv_size(self) -> int:
+        return (self.num_heads + 2 * self.num_kv_heads) * self.head_dim
+
+
+# The synthetic Qwen-style decoder of the verify benchmark (28 layers, hidden 2048, 16/8 heads).
+QWEN_SYNTHETIC = LanguageConfig(2048, 6144, 28, 16, 8, 128, 1e-6, 1e6, 151_936)
+
+
+@dataclass
+class LayerWeights:
+    input_norm: torch.Tensor   # [hidden]
+    qkv: torch.Tensor          # [(H + 2KV) * D, hidden]  (q | k | v rows, language.py:237)
+    q_norm: torch.Tensor       # [D]
+    k_norm: torch.Tensor       # [D]
+    o: torch.Tensor            # [hidden, H * D]
+    post_norm: torch.Tensor    # [hidden]
+    gate_up: torch.Tensor      # [2 * intermediate, hidden]  (gate rows then up rows, language.py:238)
+    down: torch.Tensor         # [hidden, intermediate]
+
+
+@dataclass
+class LanguageWeights:
+    embed: torch.Tensor        # [vocab, hidden]
+    layers: list[LayerWeights]
+    final_norm: torch.Tensor   # [hidden]
+    lm_head: torch.Tensor      # [vocab, hidden]
+    rope_cos: torch.Tensor     # [max_positions, D/2] bf16
+    rope_sin: torch.Tensor
+
+    def to(self, device) -> "LanguageWeights":
+        mv = lambda t: t.to(device)
+        return LanguageWeights(
+            mv(self.embed), [LayerWeights(*(mv(getattr(l, f)) for f in LayerWeights.__dataclass_fields__)) for l in self.layers],
+            mv(self.final_norm), mv(self.lm_head), mv(self.rope_cos), mv(self.rope_sin),
+        )
+
+
+def rope_tables(config: LanguageConfig, max_positions: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """language.py:160-170: fp32 angles ``position * theta^(-2i/D)``, cos/sin, stored as bf16."""
+    inv_freq = 1.0 / (config.rope_theta ** (torch.arange(0, config.head_dim, 2, dtype=torch.float) / config.head_dim))
+    freqs = torch.outer(torch.arange(max_positions, dtype=torch.float), inv_freq)
+    return freqs.cos().to(torch.bfloat16), freqs.sin().to(torch.bfloat16)
+
+
+def random_weights(config: LanguageConfig, max_positions: int, *, seed: int = 0, device="cuda",
+                   std: float = 0.02) -> LanguageWeights:
+    """Random-init weights (no checkpoint): matrices ~N(0, std), norm weights ~U(0.5, 1.5)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    c = config
+
+    def mat(*shape):
+        return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
+
+    def norm(n):
+        return (0.5 + torch.rand(n, generator=g, device=device)).to(torch.bfloat16)
+
+    layers = [
+        LayerWeights(
+            norm(c.hidden_size), mat(c.qkv_size, c.hidden_size), norm(c.head_dim), norm(c.head_dim),
+            mat(c.hidden_size, c.num_heads * c.head_dim), norm(c.hidden_size),
+            mat(2 * c.intermediate_size, c.hidden_size), mat(c.hidden_size, c.intermediate_size),
+        )
+        for _ in range(c.num_layers)
+    ]
+    cos, sin = rope_tables(c, max_positions)
+    return LanguageWeights(mat(c.vocab_size, c.hidden_size), layers, norm(c.hidden_size),
+                           mat(c.vocab_size, c.hidden_size), cos.to(device), sin.to(device))
+
+
+@dataclass
+class ExtendBatch:
+    """One verify step: every sequence brings the same number S of new tokens (language.py:122-136).
+
+    The reference passes ``embeds``; this build takes the token ``ids`` and fuses the embedding
+    gather into the first norm (``embeds`` may be given instead)."""
+
+    ids: torch.Tensor | None  # int64 [B * S]
+    positions: torch.Tensor   # int64 [B * S]
+    slots: torch.Tensor       # int64 [B * S]
+    seq_lens: torch.Tensor    # int32 [B], including the S new tokens
+    block_table: torch.Tensor  # int32 [B, max_blocks]
+    tokens_per_seq: int
+    embeds: torch.Tensor | None = None  # bf16 [B * S, hidden]
+
+
+@dataclass
+class StepBuffers:
+    """Every intermediate of one forward, allocated once for up to ``max_tokens`` rows."""
+
+    residual: torch.Tensor
+    h: torch.Tensor
+    qkv: torch.Tensor
+    q: torch.Tensor
+    attn: torch.Tensor
+    act: torch.Tensor
+    attn_workspace: torch.Tensor
+    head_workspace: torch.Tensor
+    predicted: torch.Tensor
+    max_tokens: int
+    max_seq_len: int
+    max_batch: int = field(default=0)
+
+    @classmethod
+    def allocate(cls, config: LanguageConfig, max_batch: int, tokens_per_seq: int, max_seq_len: int,
+                 device) -> "StepBuffers":
+        t = max_batch * tokens_per_seq
+        bf = dict(dtype=torch.bfloat16, device=device)
+        return cls(
+            residual=torch.zeros(t, config.hidden_size, **bf), h=torch.zeros(t, config.hidden_size, **bf),
+            qkv=torch.zeros(t, config.qkv_size, **bf),
+            q=torch.zeros(max_batch, tokens_per_seq, config.num_heads, config.head_dim, **bf),
+            attn=torch.zeros(max_batch, tokens_per_seq, config.num_heads, config.head_dim, **bf),
+            act=torch.zeros(t, config.intermediate_size, **bf),
+            attn_workspace=torch.zeros(max(attention.workspace_bytes(max_batch, config.num_kv_heads, max_seq_len), 1),
+                                       dtype=torch.uint8, device=device),
+            head_workspace=torch.zeros(max(lm_head.workspace_bytes(t, config.vocab_size), 1), dtype=torch.uint8,
+                                       device=device),
+            predicted=torch.zeros(t, dtype=torch.int64, device=device),
+            max_tokens=t, max_seq_len=max_seq_len, max_batch=max_batch,
+        )
+
+
+class LanguageModel:
+    """Verify forward (``extend``) and LM head of the decoder on gfx950 kernels."""
+
+    def __init__(self, config: LanguageConfig, weights: LanguageWeights):
+        self.config = config
+        self.weights = weights
+
+    def extend(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers | None = None) -> torch.Tensor:
+        """``[B * S, hidden]``: the final-norm hidden state of every new token (language.py:201-211).
+        K/V of the new tokens are written into ``cache`` at ``batch.slots``."""
+        buffers = self._buffers(batch, cache, buffers)
+        self.embed(batch, buffers)
+        self.run_layers(batch, cache, buffers, 0, self.config.num_layers, first_norm_done=True)
+        return self.final_norm(batch, buffers)
+
+    def _buffers(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers | None) -> StepBuffers:
+        _lib.require_gpu(batch.positions, batch.slots, batch.seq_lens, batch.block_table, name="extend")
+        b, s = batch.block_table.shape[0], batch.tokens_per_seq
+        if buffers is None:
+            buffers = StepBuffers.allocate(self.config, b, s, batch.block_table.shape[1] * cache.block_size,
+                                           batch.positions.device)
+        _lib.require(b * s <= buffers.max_tokens and b <= buffers.max_batch, "extend: batch larger than the buffers")
+        return buffers
+
+    def embed(self, batch: ExtendBatch, buffers: StepBuffers) -> None:
+        """residual = embed_tokens(ids) (decode_graph.py:164); h = layer 0's input norm of it."""
+        c, w = self.config, self.weights
+        t = batch.block_table.shape[0] * batch.tokens_per_seq
+        res, h = buffers.residual[:t], buffers.h[:t]
+        stream = _lib.stream(batch.positions.device)
+        if batch.ids is not None:
+            _lib.call("oxr_embed_rms_norm", batch.ids.data_ptr(), t, w.embed.data_ptr(), c.vocab_size, c.hidden_size,
+                      w.layers[0].input_norm.data_ptr(), float(c.rms_norm_eps), res.data_ptr(), h.data_ptr(), stream)
+        else:
+            res.copy_(batch.embeds)
+            self._norm(res, w.layers[0].input_norm, h, stream)
+
+    def _norm(self, x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, stream: int) -> None:
+        c = self.config
+        _lib.call("oxr_rms_norm", x.data_ptr(), x.stride(0), x.shape[0], c.hidden_size, weight.data_ptr(),
+                  float(c.rms_norm_eps), out.data_ptr(), out.stride(0), stream)
+
+    def run_layers(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers, start: int, stop: int, *,
+                   first_norm_done: bool = False) -> None:
+        """Layers ``[start, stop)`` on ``buffers.residual`` (the residual stream after the previous
+        layer's MLP add); afterwards it holds the residual after layer ``stop - 1``."""
+        c, w = self.config, self.weights
+        b, s = batch.block_table.shape[0], batch.tokens_per_seq
+        t = b * s
+        stream = _lib.stream(batch.positions.device)
+        res, h = buffers.residual[:t], buffers.h[:t]
+        qkv, q = buffers.qkv[:t], buffers.q[:b]
+        attn, act = buffers.attn[:b], buffers.act[:t]
+        q_flat = q.view(t, c.num_heads, c.head_dim)
+        attn_flat = attn.view(t, c.num_heads * c.head_dim)
+        num_slots = cache.num_blocks * cache.block_size
+        max_seq_len = min(buffers.max_seq_len, batch.block_table.shape[1] * cache.block_size)
+        eps = float(c.rms_norm_eps)
+        for index in range(start, stop):
+            layer = w.layers[index]
+            if not (first_norm_done and index == start):
+                self._norm(res, layer.input_norm, h, stream)
+            gemm.linear(h, layer.qkv, out=qkv)
+            k_cache, v_cache = cache.k[index], cache.v[index]
+            _lib.call(
+                "oxr_qk_norm_rope_store_at", qkv.data_ptr(), layer.q_norm.data_ptr(), layer.k_norm.data_ptr(),
+                w.rope_cos.data_ptr(), w.rope_sin.data_ptr(), w.rope_cos.shape[0], batch.positions.data_ptr(), eps,
+                k_cache.data_ptr(), v_cache.data_ptr(), batch.slots.data_ptr(), num_slots, t, c.num_heads,
+                c.num_kv_heads, c.head_dim, q_flat.data_ptr(), None, None, stream,
+            )
+            attention.paged_extend(q, k_cache, v_cache, batch.seq_lens, batch.block_table, scale=c.head_dim ** -0.5,
+                                   max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace)
+            gemm.linear_add_(res, attn_flat, layer.o)
+            self._norm(res, layer.post_norm, h, stream)
+            gemm.linear_silu_mul(h, layer.gate_up, out=act)
+            gemm.linear_add_(res, act, layer.down)
+
+    def final_norm(self, batch: ExtendBatch, buffers: StepBuffers) -> torch.Tensor:
+        t = batch.block_table.shape[0] * batch.tokens_per_seq
+        h = buffers.h[:t]
+        self._norm(buffers.residual[:t], self.weights.final_norm, h, _lib.stream(batch.positions.device))
+        return h
+
+    def logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """bf16 ``hidden @ lm_head^T`` (language.py:213-214)."""
+        return lm_head.logits(hidden, self.weights.lm_head)
+
+    def greedy(self, hidden: torch.Tensor, buffers: StepBuffers | None = None) -> torch.Tensor:
+        """``logits(hidden).argmax(-1)`` without materialising the logits (decode_graph.py:167)."""
+        if buffers is None:
+            return lm_head.lm_head_argmax(hidden, self.weights.lm_head)[0]
+        t = hidden.shape[0]
+        return lm_head.lm_head_argmax(hidden, self.weights.lm_head, predicted=buffers.predicted[:t],
+                                      workspace=buffers.head_workspace)[0]
