@@ -1,0 +1,266 @@
+"""Benchmark: the full HIP-graph speculative verify step on one MI355X.
+
+Workload (BASELINE config 5 at its headline point): a random-init 28-layer Qwen-style decoder
+(hidden 2048, 16 q / 8 kv heads, head_dim 128, q/k RMSNorm, SwiGLU 6144, vocab 151,936, bf16),
+B=8 sequences, k=3 drafts (S=4 verify tokens per sequence), KV length 4096 per sequence at the
+start, block size 16, pages drawn from a random permutation of the pool, histories of 1024
+table-like generated ids (fragments of period 8-24).  One step = drafting + row assembly +
+28-layer forward + LM head/argmax + acceptance + rollback, all in one HIP graph replay;
+inputs and state are resident in HBM.
+
+Prints one JSON line: accepted tokens/s (the metric), verify-step latency, the step's HBM
+roofline fraction, the dominant kernel's roofline entry (paged verify attention at one layer's
+shape, timed with HIP events on its own stream) and the CPU baseline (the oracle's torch
+restatement of the same step on this host's cores).
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PKG = "oxr-inference_amd"
+language = importlib.import_module(f"{PKG}.language")
+kv_cache = importlib.import_module(f"{PKG}.kv_cache")
+decode_graph = importlib.import_module(f"{PKG}.decode_graph")
+attention = importlib.import_module(f"{PKG}.attention")
+workloads = importlib.import_module(f"{PKG}.workloads")
+
+METRIC = "accepted tokens/sec + verify-step latency (us) at B=8,k=3; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*parts) -> None:
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def build_workload(args, device):
+    config = language.QWEN_SYNTHETIC
+    if args.layers != config.num_layers:
+        config = language.LanguageConfig(**{**config.__dict__, "num_layers": args.layers})
+    rng = np.random.default_rng(args.seed)
+    steps_total = args.warmup + args.steps + 4
+    S = args.k + 1
+    bs = args.block_size
+    max_len = args.ctx + S * steps_total + S
+    width = -(-max_len // bs)
+    num_blocks = args.batch * width + 16
+    weights = language.random_weights(config, max_len + 64, seed=args.seed, device=device)
+    model = language.LanguageModel(config, weights)
+    cache = kv_cache.KVCache(config.num_layers, config.num_kv_heads, config.head_dim, num_blocks, block_size=bs)
+    g = torch.Generator(device=device).manual_seed(args.seed + 1)
+    for layer in range(config.num_layers):  # context K/V ~N(0, 1), as keys after the q/k norm
+        cache.k[layer].normal_(generator=g)
+        cache.v[layer].normal_(generator=g)
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    table = perm[: args.batch * width].reshape(args.batch, width)
+    histories = [workloads.repetitive_history(rng, args.history, repetitive_tail=True) for _ in range(args.batch)]
+    seq_lens = np.full(args.batch, args.ctx, dtype=np.int32)
+    return config, model, cache, table, histories, seq_lens, width
+
+
+def step_bytes(config, batch, tokens_per_seq, kv_lens_mean) -> dict:
+    """Algorithmic HBM bytes of one verify step: every weight once, the KV of every visible token
+    once per layer, the new tokens' KV written once per layer."""
+    c = config
+    layer = 2 * (c.qkv_size * c.hidden_size + c.hidden_size * c.num_heads * c.head_dim
+                 + 2 * c.intermediate_size * c.hidden_size + c.hidden_size * c.intermediate_size
+                 + 2 * c.hidden_size + 2 * c.head_dim)
+    weights = c.num_layers * layer + 2 * c.vocab_size * c.hidden_size + 2 * c.hidden_size
+    kv_token = 2 * 2 * c.num_kv_heads * c.head_dim  # K and V, bf16
+    kv_read = c.num_layers * batch * (kv_lens_mean + tokens_per_seq) * kv_token
+    kv_write = c.num_layers * batch * tokens_per_seq * kv_token
+    return {"weights": weights, "kv_read": kv_read, "kv_write": kv_write, "total": weights + kv_read + kv_write}
+
+
+def time_attention(config, cache, loop, iters: int = 50) -> dict:
+    """The dominant kernel (paged verify attention, one fused launch) at the step's layer shape,
+    timed with HIP events on the stream it is launched on."""
+    b, s = loop.batch, loop.tokens_per_seq
+    seq = (loop.seq_len + s).to(torch.int32)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn(b, s, config.num_heads, config.head_dim, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    max_seq_len = loop.block_table.shape[1] * cache.block_size
+    ws = torch.zeros(attention.workspace_bytes(b, config.num_kv_heads, max_seq_len), dtype=torch.uint8, device="cuda")
+    run = lambda: attention.paged_extend(q, cache.k[0], cache.v[0], seq, loop.block_table, max_seq_len=max_seq_len,
+                                         out=out, workspace=ws)
+    for _ in range(5):
+        run()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        run()
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / iters
+    kv = int(seq.sum().item()) * 2 * 2 * config.num_kv_heads * config.head_dim
+    qo = 2 * 2 * b * s * config.num_heads * config.head_dim
+    return {"us": us, "bytes": kv + qo}
+
+
+def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict:
+    """The oracle's torch-CPU restatement of one verify step (oracle/decoder.py) on this host."""
+    from oracle import decoder as oracle_decoder  # the CPU baseline leg only
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    weights = model.weights.to("cpu")
+    # Compact copy of the pages the batch uses (the GPU pool holds many more).
+    used = np.unique(table)
+    remap = np.zeros(int(used.max()) + 1, dtype=np.int32)
+    remap[used] = np.arange(len(used), dtype=np.int32)
+    idx = torch.from_numpy(used.astype(np.int64)).cuda()
+    ck = cache.k[:, idx].cpu()
+    cv = cache.v[:, idx].cpu()
+    ctable = remap[table]
+    hist = [list(map(int, h)) for h in histories]
+    times, committed = [], []
+    for i in range(args.cpu_warmup + args.cpu_steps):
+        t0 = time.perf_counter()
+        _, _, taken, _ = oracle_decoder.verify_step(config, weights, hist, seq_lens, ctable, args.k, args.max_n, ck, cv,
+                                                    args.block_size)
+        dt = time.perf_counter() - t0
+        if i >= args.cpu_warmup:
+            times.append(dt)
+            committed.append(sum(len(t) for t in taken))
+        log(f"cpu step {i}: {dt:.3f} s")
+    med = float(np.median(times))
+    model_name = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": float(np.mean(committed)) / med, "unit": "accepted tokens/s", "cores": torch.get_num_threads(),
+        "kind": "port", "ms_per_step": med * 1000.0,
+        "sample": f"{args.cpu_steps} timed steps (+{args.cpu_warmup} warm-up) of the same B={args.batch} step, median; "
+                  f"torch {torch.__version__} CPU, {model_name}",
+    }
+
+
+def main() -> int:
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--k", type=int, default=3)
+    p.add_argument("--ctx", type=int, default=4096)
+    p.add_argument("--layers", type=int, default=28)
+    p.add_argument("--history", type=int, default=1024)
+    p.add_argument("--block-size", type=int, default=16)
+    p.add_argument("--max-n", type=int, default=4)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-steps", type=int, default=5)
+    p.add_argument("--cpu-warmup", type=int, default=1)
+    args = p.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the verify step is "
+              "single-GPU and no multi-GPU path is built.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+
+    log("building workload")
+    config, model, cache, table, histories, seq_lens, width = build_workload(args, device)
+    loop = decode_graph.VerifyLoop(model, cache, batch=args.batch, k=args.k, max_n=args.max_n,
+                                   history_capacity=args.history + (args.k + 1) * (args.steps + args.warmup + 8),
+                                   table_width=width, device=device)
+    loop.load(histories, seq_lens, table)
+    log("capturing graph")
+    loop.capture()
+    for _ in range(args.warmup):
+        loop.replay()
+    torch.cuda.synchronize()
+    seq_before = loop.seq_len.clone()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        loop.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    seq_after = loop.seq_len.clone()
+    committed = int((seq_after - seq_before).sum().item())
+    accepted_drafts = committed - args.batch * args.steps
+    kv_mean = float((seq_before.float().mean() + seq_after.float().mean()).item() / 2)
+    traffic = step_bytes(config, args.batch, args.k + 1, kv_mean)
+    step_gbs = traffic["total"] / (ms * 1e-3) / 1e9
+    log(f"{ms * 1000:.1f} us/step, {committed} tokens committed, step HBM {step_gbs:.0f} GB/s")
+
+    attn = time_attention(config, cache, loop)
+    attn_gbs = attn["bytes"] / (attn["us"] * 1e-6) / 1e9
+    log(f"attention kernel {attn['us']:.2f} us, {attn_gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(config, model, cache, table, histories, seq_lens, args)
+
+    s = args.k + 1
+    result = {
+        "metric": METRIC,
+        "value": committed / (args.steps * ms * 1e-3),
+        "unit": "accepted tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random context K/V, repetitive table-like histories)",
+        "config": {
+            "workload": "full hipGraph verify step (BASELINE config 5)", "batch": args.batch, "k": args.k,
+            "tokens_per_seq": s, "ctx_start": args.ctx, "layers": config.num_layers, "hidden": config.hidden_size,
+            "heads": f"{config.num_heads}/{config.num_kv_heads}", "head_dim": config.head_dim,
+            "intermediate": config.intermediate_size, "vocab": config.vocab_size, "block_size": args.block_size,
+            "history": args.history, "max_n": args.max_n,
+        },
+        "verify_step_us": ms * 1000.0,
+        "verified_tokens_per_s": args.batch * s / (ms * 1e-3),
+        "accepted_drafts_per_step": accepted_drafts / args.steps,
+        "step_roofline": {"bound": "hbm", "bytes": traffic["total"], "achieved": step_gbs, "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
+        "roofline": {"kernel": "paged_extend_partial_kernel (paged verify attention, one layer)", "bound": "hbm",
+                     "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": attn_gbs / HBM_PEAK_GBS,
+                     "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"], "traffic": None},
+        "cpu_baseline": cpu,
+        "wall_s_timed": wall,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

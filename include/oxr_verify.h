@@ -161,7 +161,10 @@ int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, 
  * max_seq_len <= table_stride * block_size; contexts longer than max_seq_len
  * are clamped to it.  workspace: at least
  * oxr_paged_extend_workspace_bytes(batch, KV, max_seq_len) bytes of device
- * memory (partials of the context split; no initial contents needed).
+ * memory holding the context split's partials and one arrival counter per
+ * (sequence, kv head).  It must be zero-filled before its first use; every
+ * call leaves it ready for the next.  Calls that overlap in time must not
+ * share a workspace.
  */
 size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
 int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache, const int32_t* seq_lens,

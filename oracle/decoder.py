@@ -61,15 +61,16 @@ def paged_extend(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
 
 
 def qk_norm_rope_store(qkv, q_weight, k_weight, cos, sin, eps, k_cache, v_cache, slots, H, KV, D):
-    """kernels.py:181-203 via the numpy restatement (bit-identical to the reference function)."""
-    kc = _bits(k_cache).copy()
-    vc = _bits(v_cache).copy()
-    q, _, _ = norm_rope.qk_norm_rope_store(
-        _bits(qkv), _bits(q_weight), _bits(k_weight), _bits(cos), _bits(sin), eps, kc, vc, slots.numpy(), H, KV, D,
-        need_kv=False,
-    )
-    k_cache.copy_(_from_bits(kc).view(k_cache.shape))
-    v_cache.copy_(_from_bits(vc).view(v_cache.shape))
+    """kernels.py:181-203: q/k through ``oracle.norm_rope.norm_rope`` (bit-identical to the
+    reference function), then the cache rows at ``slots`` are written (kernels.py:200-202)."""
+    n = qkv.shape[0]
+    heads = _bits(qkv).reshape(n, H + 2 * KV, D)
+    c, s_ = _bits(cos), _bits(sin)
+    q = norm_rope.norm_rope(heads[:, :H], _bits(q_weight), c, s_, eps)
+    k = norm_rope.norm_rope(heads[:, H : H + KV], _bits(k_weight), c, s_, eps)
+    flat = (-1, KV, D)
+    k_cache.view(flat)[slots] = _from_bits(k)
+    v_cache.view(flat)[slots] = _from_bits(np.ascontiguousarray(heads[:, H + KV :]))
     return _from_bits(q)
 
 

@@ -27,8 +27,8 @@ def paged_extend(
     Returns ``[B, S, heads, dim]``.
 
     ``max_seq_len`` bounds every ``seq_lens[b]`` (default: the block table's span) and sizes the
-    context split; ``out`` and ``workspace`` (bytes from :func:`workspace_bytes`) may be passed in
-    to avoid allocations."""
+    context split; ``out`` and ``workspace`` (bytes from :func:`workspace_bytes`, zero-filled before
+    its first use and left zeroed by every call) may be passed in to avoid allocations."""
     device = _lib.require_gpu(q, k_cache, v_cache, seq_lens, block_table, name="paged_extend")
     _lib.require(q.dim() == 4 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [B, S, H, D]")
     b, s, h, d = q.shape
@@ -49,7 +49,8 @@ def paged_extend(
         out = torch.empty_like(q)
     need = workspace_bytes(b, kv, max_seq_len)
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)  # counters start at zero
+    _lib.require(workspace.numel() * workspace.element_size() >= need, "paged_extend: workspace too small")
     _lib.call(
         "oxr_paged_extend", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), seq_lens.data_ptr(),
         block_table.data_ptr(), block_table.stride(0), b, s, h, kv, d, block_size, num_blocks, max_seq_len,

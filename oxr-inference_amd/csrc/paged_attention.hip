@@ -10,8 +10,11 @@
 // with R = S * (H / KV) query rows (8 at S=4, 16/8 heads), against contexts
 // of thousands of tokens, so the context is split into chunks of kChunk
 // tokens and every (chunk, kv head, sequence) is one single-wave workgroup.
-// Each writes an unnormalised partial (running max m, sum l, O[R][128]) and a
-// second kernel merges the chunks with the usual log-sum-exp rescaling.
+// Each writes an unnormalised partial (running max m, sum l, O[R][128]) and
+// counts itself on a per-(sequence, kv head) counter; the workgroup that
+// arrives last merges the chunks with the usual log-sum-exp rescaling and
+// resets the counter, so one launch does the whole op.  A context that fits
+// in one chunk is normalised and stored directly.
 //
 // Per wave, 32 keys at a time (two 16-key MFMA tiles):
 //   S^T tile = K[16 keys x 128] * Q^T        4 x v_mfma_f32_16x16x32_bf16 per tile
@@ -74,7 +77,8 @@ __global__ __launch_bounds__(64) void paged_extend_partial_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table, int64_t table_stride, int S,
     int H, int KV, int log2_bs, int64_t num_blocks, float scale_log2, int max_seq_len, int max_chunks,
-    float* __restrict__ part_o, float* __restrict__ part_ml) {
+    float* __restrict__ part_o, float* __restrict__ part_ml, int32_t* __restrict__ counters,
+    bf16_t* __restrict__ out) {
   __shared__ __align__(16) uint16_t vt[kD * kVPitch];
 
   const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -173,44 +177,57 @@ __global__ __launch_bounds__(64) void paged_extend_partial_kernel(
 
   float l_tot = l_run + shfl_xor_f(l_run, 16);
   l_tot += shfl_xor_f(l_tot, 32);
+  const int nc = (L + kChunk - 1) / kChunk;
+  if (nc == 1) {
+    // The whole context fits one chunk: normalise and store directly.
+    if (r < R) {
+      const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+      const int s = r / G, hh = r % G;
+      bf16_t* dst = out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const f32x4 v = o[dt] * inv;
+        *reinterpret_cast<u32x2*>(dst + dt * 16 + 4 * g) = u32x2{pack_bf(v[0], v[1]), pack_bf(v[2], v[3])};
+      }
+    }
+    return;
+  }
+  const int64_t unit0 = ((int64_t)b * KV + kvh) * max_chunks;
   if (r < R) {
-    const int64_t unit = ((int64_t)b * KV + kvh) * max_chunks + chunk;
-    float* dst = part_o + (unit * kRows + r) * kD;
+    float* dst = part_o + ((unit0 + chunk) * kRows + r) * kD;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(dst + dt * 16 + 4 * g) = o[dt];
     if (g == 0) {
-      part_ml[(unit * kRows + r) * 2 + 0] = m_run;
-      part_ml[(unit * kRows + r) * 2 + 1] = l_tot;
+      part_ml[((unit0 + chunk) * kRows + r) * 2 + 0] = m_run;
+      part_ml[((unit0 + chunk) * kRows + r) * 2 + 1] = l_tot;
     }
   }
-}
-
-__global__ __launch_bounds__(256) void paged_extend_merge_kernel(const float* __restrict__ part_o,
-                                                                 const float* __restrict__ part_ml,
-                                                                 const int32_t* __restrict__ seq_lens, int S, int H,
-                                                                 int KV, int chunk_tokens, int max_seq_len,
-                                                                 int max_chunks, bf16_t* __restrict__ out) {
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  const int G = H / KV, R = S * G;
-  const int L = min(seq_lens[b], max_seq_len);
-  const int nc = L > 0 ? (L + chunk_tokens - 1) / chunk_tokens : 0;
-  const int64_t unit0 = ((int64_t)b * KV + kvh) * max_chunks;
-  for (int idx = threadIdx.x; idx < R * (kD / 4); idx += blockDim.x) {
-    const int r = idx / (kD / 4), d0 = (idx % (kD / 4)) * 4;
+  // The last chunk of this (sequence, kv head) to finish merges all of them:
+  // release the partial, count it, and the workgroup that brings the count to
+  // nc acquires every partial and resets the counter for the next launch.
+  __threadfence();
+  int arrived = 0;
+  if (lane == 0) arrived = atomicAdd(counters + (int64_t)b * KV + kvh, 1);
+  arrived = __shfl(arrived, 0, kWave);
+  if (arrived != nc - 1) return;
+  __threadfence();
+  if (lane == 0) counters[(int64_t)b * KV + kvh] = 0;
+  for (int idx = lane; idx < R * (kD / 4); idx += kWave) {
+    const int rr = idx / (kD / 4), d0 = (idx % (kD / 4)) * 4;
     float mmax = -INFINITY;
-    for (int c = 0; c < nc; ++c) mmax = fmaxf(mmax, part_ml[((unit0 + c) * kRows + r) * 2]);
+    for (int c = 0; c < nc; ++c) mmax = fmaxf(mmax, __builtin_nontemporal_load(part_ml + ((unit0 + c) * kRows + rr) * 2));
     const float m_use = (mmax == -INFINITY) ? 0.f : mmax;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     float lsum = 0.f;
     for (int c = 0; c < nc; ++c) {
-      const float m = part_ml[((unit0 + c) * kRows + r) * 2];
-      const float w = exp2f(m - m_use);
-      lsum += part_ml[((unit0 + c) * kRows + r) * 2 + 1] * w;
-      const f32x4 v = *reinterpret_cast<const f32x4*>(part_o + ((unit0 + c) * kRows + r) * kD + d0);
+      const float* ml = part_ml + ((unit0 + c) * kRows + rr) * 2;
+      const float w = exp2f(__builtin_nontemporal_load(ml) - m_use);
+      lsum += __builtin_nontemporal_load(ml + 1) * w;
+      const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(part_o + ((unit0 + c) * kRows + rr) * kD + d0));
       acc += v * w;
     }
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-    const int s = r / G, hh = r % G;
+    const int s = rr / G, hh = rr % G;
     uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
     dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
     dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
@@ -228,7 +245,7 @@ extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv
   using namespace oxr;
   if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0) return 0;
   const size_t units = (size_t)batch * num_kv_heads * chunks_for(max_seq_len);
-  return units * kRows * (kD + 2) * sizeof(float);
+  return units * kRows * (kD + 2) * sizeof(float) + (size_t)batch * num_kv_heads * sizeof(int32_t);
 }
 
 extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache,
@@ -256,14 +273,11 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
   while ((1 << log2_bs) < block_size) ++log2_bs;
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)batch * num_kv_heads * max_chunks * kRows * kD;
+  int32_t* counters = reinterpret_cast<int32_t*>(part_ml + (size_t)batch * num_kv_heads * max_chunks * kRows * 2);
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(paged_extend_partial_kernel<kChunkTokens>, dim3(max_chunks, num_kv_heads, batch), dim3(64), 0,
-                     s, q, k_cache, v_cache, seq_lens, block_table, table_stride, tokens_per_seq, num_heads,
-                     num_kv_heads, log2_bs, num_blocks, scale_log2, max_seq_len, max_chunks, part_o, part_ml);
-  int status = OXR_LAUNCH_STATUS();
-  if (status) return status;
-  hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(256), 0, s, part_o, part_ml,
-                     seq_lens, tokens_per_seq, num_heads, num_kv_heads, kChunkTokens, max_seq_len, max_chunks, out);
+                     (hipStream_t)stream, q, k_cache, v_cache, seq_lens, block_table, table_stride, tokens_per_seq,
+                     num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2, max_seq_len, max_chunks, part_o,
+                     part_ml, counters, out);
   return OXR_LAUNCH_STATUS();
 }
