@@ -157,14 +157,12 @@ int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, 
  * in the cache); block_table int32 [B, table_stride].  Token s of sequence b
  * attends keys [0, seq_lens[b] - S + s] of kv head h / (H / KV) with scores
  * q.k * scale and an fp32 softmax; out bf16 [B, S, H, 128].
- * Requires H % KV == 0, S * (H / KV) <= 16, block_size a power of two,
+ * Requires H % KV == 0, S * (H / KV) <= 16, block_size a power of two >= 16,
  * max_seq_len <= table_stride * block_size; contexts longer than max_seq_len
  * are clamped to it.  workspace: at least
  * oxr_paged_extend_workspace_bytes(batch, KV, max_seq_len) bytes of device
- * memory holding the context split's partials and one arrival counter per
- * (sequence, kv head).  It must be zero-filled before its first use; every
- * call leaves it ready for the next.  Calls that overlap in time must not
- * share a workspace.
+ * memory for the context split's partials (no initial contents needed; calls
+ * that overlap in time must not share a workspace).
  */
 size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
 int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache, const int32_t* seq_lens,

@@ -1,7 +1,7 @@
 """Multi-query causal paged attention: the drop-in for attention.paged_extend (oxr_runtime/attention.py:96-109).
 
 Runs the gfx950 kernels of csrc/paged_attention.hip (MFMA QK^T and PV tiles, context split
-across single-wave workgroups, log-sum-exp merge).  Only the verify-step entry point is
+across 8-wave workgroups merged on chip, then a small log-sum-exp merge of the splits).  Only the verify-step entry point is
 provided; the reference's prefill/vision/decode entry points (``varlen``,
 ``varlen_bidirectional``, ``paged_decode``, ``rotary``) are outside this build.
 """
@@ -27,8 +27,8 @@ def paged_extend(
     Returns ``[B, S, heads, dim]``.
 
     ``max_seq_len`` bounds every ``seq_lens[b]`` (default: the block table's span) and sizes the
-    context split; ``out`` and ``workspace`` (bytes from :func:`workspace_bytes`, zero-filled before
-    its first use and left zeroed by every call) may be passed in to avoid allocations."""
+    context split; ``out`` and ``workspace`` (bytes from :func:`workspace_bytes`) may be passed in to
+    avoid allocations."""
     device = _lib.require_gpu(q, k_cache, v_cache, seq_lens, block_table, name="paged_extend")
     _lib.require(q.dim() == 4 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [B, S, H, D]")
     b, s, h, d = q.shape
@@ -49,7 +49,7 @@ def paged_extend(
         out = torch.empty_like(q)
     need = workspace_bytes(b, kv, max_seq_len)
     if workspace is None:
-        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)  # counters start at zero
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
     _lib.require(workspace.numel() * workspace.element_size() >= need, "paged_extend: workspace too small")
     _lib.call(
         "oxr_paged_extend", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), seq_lens.data_ptr(),

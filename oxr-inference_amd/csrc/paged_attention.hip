@@ -8,27 +8,32 @@
 //
 // Work split.  A verify step has only B * KV (sequence, kv-head) pairs, each
 // with R = S * (H / KV) query rows (8 at S=4, 16/8 heads), against contexts
-// of thousands of tokens, so the context is split into chunks of kChunk
-// tokens and every (chunk, kv head, sequence) is one single-wave workgroup.
-// Each writes an unnormalised partial (running max m, sum l, O[R][128]) and
-// counts itself on a per-(sequence, kv head) counter; the workgroup that
-// arrives last merges the chunks with the usual log-sum-exp rescaling and
-// resets the counter, so one launch does the whole op.  A context that fits
-// in one chunk is normalised and stored directly.
+// of thousands of tokens.  Each pair's context is cut into `splits` ranges so
+// that about 256 workgroups (one per CU) cover the batch; a workgroup is 8
+// waves that walk its range in interleaved 32-key steps (the 8 waves read
+// neighbouring keys of the same pages at the same time).  The 8 waves'
+// (max, sum, O) are merged on chip through LDS and written as the split's
+// partial; a second small kernel merges the splits.  (A "last workgroup
+// merges" scheme in one kernel needs a device-scope release/acquire per
+// workgroup, i.e. an L2 writeback + invalidate across XCDs, which measured
+// ~70 us per launch here -- far more than a second launch.)  A context that
+// fits one split is stored directly by the main kernel.
 //
-// Per wave, 32 keys at a time (two 16-key MFMA tiles):
-//   S^T tile = K[16 keys x 128] * Q^T        4 x v_mfma_f32_16x16x32_bf16 per tile
-//     K comes straight from the paged cache: a lane reads 64 contiguous bytes
-//     of one key row, which is exactly its MFMA A-operand fragment; Q^T is
-//     held in registers.  Lane (r = l % 16, g = l / 16) gets the scores of
-//     keys 4g..4g+3 for query row r.
+// Per wave, 32 keys at a time (two 16-key MFMA tiles), all in registers:
+//   S^T tile = K[16 keys x 128] * Q^T           4 v_mfma_f32_16x16x32_bf16 / tile
+//     A lane reads 64 contiguous bytes of one key row, which is exactly its
+//     A-operand fragment; Q^T stays in registers.  Lane (r = l % 16, g = l / 16)
+//     gets the scores of keys 4g..4g+3 of the tile for query row r.
 //   online softmax per row in the exp2 domain (scale * log2 e folded in)
+//   V^T fragments by MFMA: V[16 keys x 32 dims] times a 0/1 selector gives
+//     C[key][n] = V[key][n] (or [n + 16]) in the C layout, i.e. lane (n, g) holds
+//     keys 4g..4g+3 of dim n -- the transposed fragment the PV product needs.
+//     (Exact: each output is one bf16 value times 1 plus zeros.)  This replaces
+//     an LDS transpose: no LDS, no barriers.
 //   O^T += V^T[128 x 32 keys] * P^T             8 MFMAs (one per 16 dims)
-//     P^T is the B operand as computed (bf16), with key slot 4p + j of lane
-//     group g standing for key 16p + 4g + j; V^T goes through LDS: the 32 key
-//     rows are loaded with 128-byte-per-lane reads and written transposed, so
-//     each A fragment is two 8-byte LDS reads.
-//     Accumulators hold O^T[d][r], so the per-row rescale is a per-lane scalar.
+//     P^T is the B operand as computed (bf16), key slot 4p + j of lane group g
+//     standing for key 16p + 4g + j; accumulators hold O^T[d][r], so the
+//     per-row rescale is a per-lane scalar.
 // The next 32 keys' K and V are loaded before the current ones are used.
 #include "common.h"
 
@@ -36,58 +41,77 @@ namespace oxr {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kRows = 16;   // query rows per (sequence, kv head): one MFMA tile
-constexpr int kVPitch = 36; // LDS row pitch of V^T in bf16 (32 keys + pad, 8-byte aligned)
+constexpr int kRows = 16;  // query rows per (sequence, kv head): one MFMA tile
+constexpr uint32_t kBf16One = 0x3f80u;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 struct PairRegs {
-  u32x4 k[2][4];  // K fragments of the two 16-key tiles
-  u32x4 v[8];     // 128 contiguous bytes of one key's V row
+  u32x4 k[2][4];  // tile p: K[key 16p + r][32g + 8i .. +7], i = 0..3
+  u32x4 v[2][4];  // tile p: V[key 16p + r][32c + 8g .. +7], c = 0..3
 };
-
-__device__ __forceinline__ int64_t row_of(const int32_t* __restrict__ table_row, int tok, int log2_bs,
-                                          int64_t num_blocks) {
-  int64_t blk = table_row[tok >> log2_bs];
-  blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);  // never leave the pool
-  return (blk << log2_bs) + (tok & ((1 << log2_bs) - 1));
-}
 
 __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict__ k_cache,
                                           const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ table_row,
-                                          int t0, int L, int kvh, int KV, int log2_bs, int64_t num_blocks, int lane) {
-  const int r = lane & 15, g = lane >> 4;
+                                          int t0, int L, int kvh, int KV, int log2_bs, int64_t num_blocks, int r,
+                                          int g) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const int tok = min(t0 + 16 * p + r, L - 1);
-    const bf16_t* src = k_cache + (row_of(table_row, tok, log2_bs, num_blocks) * KV + kvh) * kD + 32 * g;
+    // A 16-key tile lies inside one page (block_size >= 16, tiles aligned to
+    // 16), so its page number is wave-uniform: one scalar load, whose wait
+    // (lgkmcnt) does not hold back the vector loads already in flight.
+    const int tok = t0 + 16 * p + r;
+    const int tile = __builtin_amdgcn_readfirstlane(min(t0 + 16 * p, L - 1));
+    int64_t blk = table_row[tile >> log2_bs];
+    blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);  // never leave the pool
+    const int64_t row = ((blk << log2_bs) + (min(tok, L - 1) & ((1 << log2_bs) - 1))) * KV + kvh;
+    const bf16_t* ks = k_cache + row * kD + 32 * g;
+    const bf16_t* vs = v_cache + row * kD + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld128_nt(src + 8 * i);
-  }
-  const int tv = t0 + (lane >> 1);
-  const bool valid = tv < L;
-  const bf16_t* src = v_cache + (row_of(table_row, min(tv, L - 1), log2_bs, num_blocks) * KV + kvh) * kD + 64 * (lane & 1);
+    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld128(ks + 8 * i);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const u32x4 x = ld128_nt(src + 8 * i);
-    pr.v[i] = valid ? x : u32x4{0u, 0u, 0u, 0u};  // keys past L contribute 0 * 0, never 0 * garbage
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 x = ld128(vs + 32 * c);
+      pr.v[p][c] = tok < L ? x : u32x4{0u, 0u, 0u, 0u};  // keys past L add 0 * 0, never 0 * garbage
+    }
   }
 }
 
-template <int kChunk>
-__global__ __launch_bounds__(64) void paged_extend_partial_kernel(
+// Selector B operand: B[k][n] = 1 where k == n + shift (k = 8g + jj, n = r).
+__device__ __forceinline__ u32x4 selector(int r, int g, int shift) {
+  const int jj = r + shift - 8 * g;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (e == jj) w[e >> 1] |= kBf16One << (16 * (e & 1));
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Upper halves (the bf16 values) of two fp32 words, packed lo | hi << 16.
+__device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
+  return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
+}
+
+constexpr int kWaves = 8;  // waves per workgroup
+
+__global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table, int64_t table_stride, int S,
-    int H, int KV, int log2_bs, int64_t num_blocks, float scale_log2, int max_seq_len, int max_chunks,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int32_t* __restrict__ counters,
-    bf16_t* __restrict__ out) {
-  __shared__ __align__(16) uint16_t vt[kD * kVPitch];
+    int H, int KV, int log2_bs, int64_t num_blocks, float scale_log2, int max_seq_len, int splits,
+    float* __restrict__ part_o, float* __restrict__ part_ml, bf16_t* __restrict__ out) {
+  __shared__ float s_o[kWaves][kRows][kD];
+  __shared__ float s_m[kWaves][kRows], s_l[kWaves][kRows];
 
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int L = min(seq_lens[b], max_seq_len);  // max_seq_len <= table span, checked on the host
-  const int t_begin = chunk * kChunk;
-  if (t_begin >= L) return;  // the merge reads only chunks below ceil(L / kChunk)
-  const int t_end = min(L, t_begin + kChunk);
+  // This workgroup's keys: split `split` of [0, L), in whole 32-key pairs.
+  const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
+  const int t_begin = split * span;
+  const int t_end = min(L, t_begin + span);
+  const bool single = L <= span;  // the whole context is in split 0
+  if (single && split > 0) return;
   const int G = H / KV, R = S * G;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int r = lane & 15, g = lane >> 4;
   const int32_t* table_row = block_table + (int64_t)b * table_stride;
 
@@ -104,17 +128,22 @@ __global__ __launch_bounds__(64) void paged_extend_partial_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) qf[i] = u32x4{0u, 0u, 0u, 0u};
   }
+  const u32x4 sel_lo = selector(r, g, 0), sel_hi = selector(r, g, 16);
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // The waves take pairs wave, wave + 8, ... so at any time the workgroup reads
+  // 8 neighbouring pairs of the same pages.
+  const int stride = 32 * kWaves;
+  int t0 = t_begin + 32 * wave;
   PairRegs cur, nxt;
-  load_pair(cur, k_cache, v_cache, table_row, t_begin, L, kvh, KV, log2_bs, num_blocks, lane);
-  for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-    const bool more = t0 + 32 < t_end;
-    if (more) load_pair(nxt, k_cache, v_cache, table_row, t0 + 32, L, kvh, KV, log2_bs, num_blocks, lane);
+  if (t0 < t_end) load_pair(cur, k_cache, v_cache, table_row, t0, L, kvh, KV, log2_bs, num_blocks, r, g);
+  for (; t0 < t_end; t0 += stride) {
+    const bool more = t0 + stride < t_end;
+    if (more) load_pair(nxt, k_cache, v_cache, table_row, t0 + stride, L, kvh, KV, log2_bs, num_blocks, r, g);
 
     // Scores of keys t0 + 16p + 4g + j for query row r.
     float sv[8];
@@ -145,88 +174,92 @@ __global__ __launch_bounds__(64) void paged_extend_partial_kernel(
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
     const u32x4 pb = {pack_bf(pv[0], pv[1]), pack_bf(pv[2], pv[3]), pack_bf(pv[4], pv[5]), pack_bf(pv[6], pv[7])};
 
-    // V^T into LDS: this lane holds dims 64 * (lane & 1) + [0, 64) of key lane >> 1.
-    __syncthreads();
-    {
-      const int key = lane >> 1, d0 = 64 * (lane & 1);
+    // V^T fragments: dims 32c + [0, 16) and 32c + [16, 32) of both tiles.
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w[4] = {cur.v[i].x, cur.v[i].y, cur.v[i].z, cur.v[i].w};
+    for (int c = 0; c < 4; ++c) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vt[(d0 + 8 * i + 2 * e) * kVPitch + key] = (uint16_t)(w[e] & 0xffffu);
-          vt[(d0 + 8 * i + 2 * e + 1) * kVPitch + key] = (uint16_t)(w[e] >> 16);
-        }
+      for (int half = 0; half < 2; ++half) {
+        const u32x4 sel = half ? sel_hi : sel_lo;
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 v0 = mfma_16x16x32(cur.v[0][c], sel, z);
+        const f32x4 v1 = mfma_16x16x32(cur.v[1][c], sel, z);
+        const u32x4 a = {pack_hi(v0[0], v0[1]), pack_hi(v0[2], v0[3]), pack_hi(v1[0], v1[1]), pack_hi(v1[2], v1[3])};
+        const int dt = 2 * c + half;
+        o[dt] = mfma_16x16x32(a, pb, o[dt] * alpha);
       }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* row = vt + (dt * 16 + r) * kVPitch;
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(row + 4 * g);
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16 + 4 * g);
-      const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
-      o[dt] = mfma_16x16x32(a, pb, o[dt]);
     }
     if (more) cur = nxt;
   }
 
+  // Merge the 8 waves on chip.
   float l_tot = l_run + shfl_xor_f(l_run, 16);
   l_tot += shfl_xor_f(l_tot, 32);
-  const int nc = (L + kChunk - 1) / kChunk;
-  if (nc == 1) {
-    // The whole context fits one chunk: normalise and store directly.
-    if (r < R) {
-      const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-      const int s = r / G, hh = r % G;
-      bf16_t* dst = out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const f32x4 v = o[dt] * inv;
-        *reinterpret_cast<u32x2*>(dst + dt * 16 + 4 * g) = u32x2{pack_bf(v[0], v[1]), pack_bf(v[2], v[3])};
-      }
-    }
-    return;
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[dt];
+  if (g == 0) {
+    s_m[wave][r] = m_run;
+    s_l[wave][r] = l_tot;
   }
-  const int64_t unit0 = ((int64_t)b * KV + kvh) * max_chunks;
-  if (r < R) {
-    float* dst = part_o + ((unit0 + chunk) * kRows + r) * kD;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(dst + dt * 16 + 4 * g) = o[dt];
-    if (g == 0) {
-      part_ml[((unit0 + chunk) * kRows + r) * 2 + 0] = m_run;
-      part_ml[((unit0 + chunk) * kRows + r) * 2 + 1] = l_tot;
-    }
-  }
-  // The last chunk of this (sequence, kv head) to finish merges all of them:
-  // release the partial, count it, and the workgroup that brings the count to
-  // nc acquires every partial and resets the counter for the next launch.
-  __threadfence();
-  int arrived = 0;
-  if (lane == 0) arrived = atomicAdd(counters + (int64_t)b * KV + kvh, 1);
-  arrived = __shfl(arrived, 0, kWave);
-  if (arrived != nc - 1) return;
-  __threadfence();
-  if (lane == 0) counters[(int64_t)b * KV + kvh] = 0;
-  for (int idx = lane; idx < R * (kD / 4); idx += kWave) {
+  __syncthreads();
+  const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
+  for (int idx = tid; idx < R * (kD / 4); idx += 64 * kWaves) {
     const int rr = idx / (kD / 4), d0 = (idx % (kD / 4)) * 4;
     float mmax = -INFINITY;
-    for (int c = 0; c < nc; ++c) mmax = fmaxf(mmax, __builtin_nontemporal_load(part_ml + ((unit0 + c) * kRows + rr) * 2));
-    const float m_use = (mmax == -INFINITY) ? 0.f : mmax;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, s_m[w][rr]);
+    const float mu = (mmax == -INFINITY) ? 0.f : mmax;
+    float l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    for (int c = 0; c < nc; ++c) {
-      const float* ml = part_ml + ((unit0 + c) * kRows + rr) * 2;
-      const float w = exp2f(__builtin_nontemporal_load(ml) - m_use);
-      lsum += __builtin_nontemporal_load(ml + 1) * w;
-      const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(part_o + ((unit0 + c) * kRows + rr) * kD + d0));
-      acc += v * w;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = exp2f(s_m[w][rr] - mu);
+      l += s_l[w][rr] * wt;
+      acc += *reinterpret_cast<const f32x4*>(&s_o[w][rr][d0]) * wt;
     }
-    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    if (single) {
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const int s = rr / G, hh = rr % G;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
+      dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
+      dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
+    } else {
+      *reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kRows + rr) * kD + d0) = acc;
+      if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + ((unit0 + split) * kRows + rr) * 2) = f32x2{mmax, l};
+    }
+  }
+}
+
+// Merge of the context splits of every (sequence, kv head): one workgroup per
+// pair, one thread per 4 output dims of a row.  Sequences whose context fitted
+// one split were already stored by the main kernel.
+__global__ __launch_bounds__(256) void paged_extend_merge_kernel(const float* __restrict__ part_o,
+                                                                 const float* __restrict__ part_ml,
+                                                                 const int32_t* __restrict__ seq_lens, int S, int H,
+                                                                 int KV, int max_seq_len, int splits,
+                                                                 bf16_t* __restrict__ out) {
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int L = min(seq_lens[b], max_seq_len);
+  const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
+  if (L <= span) return;
+  const int G = H / KV, R = S * G;
+  const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
+  for (int idx = threadIdx.x; idx < R * (kD / 4); idx += blockDim.x) {
+    const int rr = idx / (kD / 4), d0 = (idx % (kD / 4)) * 4;
+    float m = -INFINITY, l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < splits; ++c) {
+      const f32x2 ml = *reinterpret_cast<const f32x2*>(part_ml + ((unit0 + c) * kRows + rr) * 2);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(part_o + ((unit0 + c) * kRows + rr) * kD + d0);
+      const float mn = fmaxf(m, ml[0]);
+      const float mu = (mn == -INFINITY) ? 0.f : mn;
+      const float a = exp2f(m - mu), w = exp2f(ml[0] - mu);
+      l = l * a + ml[1] * w;
+      acc = acc * a + v * w;
+      m = mn;
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
     const int s = rr / G, hh = rr % G;
     uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
     dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
@@ -234,9 +267,13 @@ __global__ __launch_bounds__(64) void paged_extend_partial_kernel(
   }
 }
 
-constexpr int kChunkTokens = 256;
-
-int chunks_for(int32_t max_seq_len) { return (max_seq_len + kChunkTokens - 1) / kChunkTokens; }
+// Context splits per (sequence, kv head): about one 8-wave workgroup per CU
+// over the whole batch.
+int splits_for(int32_t batch, int32_t num_kv_heads) {
+  const int64_t units = (int64_t)batch * num_kv_heads;
+  int64_t splits = (256 + units - 1) / units;
+  return (int)(splits < 1 ? 1 : (splits > 64 ? 64 : splits));
+}
 
 }  // namespace
 }  // namespace oxr
@@ -244,8 +281,8 @@ int chunks_for(int32_t max_seq_len) { return (max_seq_len + kChunkTokens - 1) / 
 extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
   using namespace oxr;
   if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0) return 0;
-  const size_t units = (size_t)batch * num_kv_heads * chunks_for(max_seq_len);
-  return units * kRows * (kD + 2) * sizeof(float) + (size_t)batch * num_kv_heads * sizeof(int32_t);
+  const size_t units = (size_t)batch * num_kv_heads * splits_for(batch, num_kv_heads);
+  return units * kRows * (kD + 2) * sizeof(float);
 }
 
 extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache,
@@ -260,24 +297,27 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
                 OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(head_dim != kD || num_heads % num_kv_heads != 0, OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(tokens_per_seq * (num_heads / num_kv_heads) > kRows, OXR_ERR_UNSUPPORTED);
-  OXR_RETURN_IF(block_size <= 0 || (block_size & (block_size - 1)) != 0, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(block_size < 16 || (block_size & (block_size - 1)) != 0, OXR_ERR_UNSUPPORTED);
   // Contexts are clamped to max_seq_len, so every key visited maps to a table entry.
   OXR_RETURN_IF((int64_t)max_seq_len > table_stride * block_size, OXR_ERR_INVALID_ARG);
   if (batch == 0) return OXR_OK;
   OXR_RETURN_IF(!q || !k_cache || !v_cache || !seq_lens || !block_table || !out, OXR_ERR_INVALID_ARG);
   const size_t need = oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
-  const int max_chunks = chunks_for(max_seq_len);
-  OXR_RETURN_IF(max_chunks > 65535 || batch > 65535, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535, OXR_ERR_UNSUPPORTED);
+  const int splits = splits_for(batch, num_kv_heads);
   int log2_bs = 0;
   while ((1 << log2_bs) < block_size) ++log2_bs;
   float* part_o = static_cast<float*>(workspace);
-  float* part_ml = part_o + (size_t)batch * num_kv_heads * max_chunks * kRows * kD;
-  int32_t* counters = reinterpret_cast<int32_t*>(part_ml + (size_t)batch * num_kv_heads * max_chunks * kRows * 2);
+  float* part_ml = part_o + (size_t)batch * num_kv_heads * splits * kRows * kD;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(paged_extend_partial_kernel<kChunkTokens>, dim3(max_chunks, num_kv_heads, batch), dim3(64), 0,
-                     (hipStream_t)stream, q, k_cache, v_cache, seq_lens, block_table, table_stride, tokens_per_seq,
-                     num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2, max_seq_len, max_chunks, part_o,
-                     part_ml, counters, out);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(paged_extend_kernel, dim3(splits, num_kv_heads, batch), dim3(64 * kWaves), 0, s, q, k_cache,
+                     v_cache, seq_lens, block_table, table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs,
+                     num_blocks, scale_log2, max_seq_len, splits, part_o, part_ml, out);
+  int status = OXR_LAUNCH_STATUS();
+  if (status || splits == 1) return status;
+  hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(256), 0, s, part_o, part_ml,
+                     seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, out);
   return OXR_LAUNCH_STATUS();
 }

@@ -69,11 +69,11 @@ def _residual_close(got: torch.Tensor, want: torch.Tensor) -> None:
     assert rel < 1.5e-2 and err.max().item() < 0.25, (rel, err.max().item())
 
 
-def _ids_agree(pred: np.ndarray, cpu_logits: torch.Tensor) -> None:
+def _ids_agree(pred: np.ndarray, cpu_logits: torch.Tensor, margin_floor: float = ATOL) -> None:
     values = cpu_logits.float().numpy()
     part = np.partition(values, -2, axis=-1)
     margin = part[:, -1] - part[:, -2]
-    sure = margin > ATOL
+    sure = margin > margin_floor
     want = cpu_logits.argmax(-1).numpy()
     assert sure.mean() > 0.5
     assert np.array_equal(pred[sure], want[sure]), (pred, want, margin)
@@ -140,7 +140,9 @@ def test_extend_end_to_end_small_model() -> None:
     assert bool((err <= layers * (ATOL + RTOL * want.float().abs())).all()), err.max().item()
     rel = (err.pow(2).sum() / want.float().pow(2).sum()).sqrt().item()
     assert rel < 2e-2, rel
-    _ids_agree(pred, oracle_decoder.logits(cpu_w, want))
+    # The untied logits carry the compounded ~1-2% error too: ids must agree where the oracle's
+    # top-2 margin is well clear of it (0.1, five times the per-op tolerance).
+    _ids_agree(pred, oracle_decoder.logits(cpu_w, want), margin_floor=0.1)
 
 
 def test_chunked_extends_equal_full_sequence() -> None:
