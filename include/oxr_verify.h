@@ -149,6 +149,16 @@ int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, 
                        const oxr_bf16* weight, float eps, oxr_bf16* residual, oxr_bf16* out, oxr_stream_t stream);
 
 /*
+ * Residual add + RMSNorm from GEMM partials (_add_rms_norm, language.py:94-99):
+ * residual = bf16(bf16(sum_s partials[s]) + residual) in place, then out =
+ * rms_norm(residual) as oxr_rms_norm.  partials fp32 [k_splits, rows, hidden]
+ * (from oxr_gemm_bf16_partial), summed in split order.
+ */
+int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t rows, int64_t hidden,
+                              oxr_bf16* residual, const oxr_bf16* weight, float eps, oxr_bf16* out,
+                              oxr_stream_t stream);
+
+/*
  * (3) Multi-query causal paged attention of the verify step.
  * Replaces attention.paged_extend (oxr_runtime/attention.py:96-109); math as
  * the reference test stub (tests/test_language_fused.py:19-28, 50-57):
@@ -190,6 +200,17 @@ int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16*
 #define OXR_EPI_ADD_RESIDUAL 3
 int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
                   int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream);
+
+/*
+ * (4a') The same GEMM for weights too narrow to fill the chip with whole-K
+ * tiles (o_proj, down_proj): k is split across workgroups and each split's
+ * fp32 sums are written to partials [k_splits, m, n]; nothing else is stored.
+ * k_splits must equal oxr_gemm_bf16_partial_splits(n, k).  The residual add
+ * + RMSNorm that follows consumes them (oxr_add_partials_rms_norm).
+ */
+int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k);
+int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
+                          float* partials, int32_t k_splits, oxr_stream_t stream);
 
 /*
  * (4b) LM head GEMM with fused vocab-wide argmax.

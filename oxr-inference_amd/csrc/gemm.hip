@@ -4,33 +4,40 @@
 // S=4) by large weights: every projection and the LM head is HBM-bound on the
 // weight read.  So the kernel is organised around streaming W exactly once:
 //
-// * A workgroup owns one tile of 16 * NA weight rows (output columns) and all
-//   M <= 16 * NB token rows.  Its kSplit waves split K; each wave streams its
-//   slice of the tile's rows with 64-byte-per-lane loads that are directly the
-//   A-operand fragments of v_mfma_f32_16x16x32_bf16 (lane (r, g) holds
-//   W[row r][k + 32g .. 32g + 31], i.e. four MFMA k-steps), prefetching the
-//   next 128 k while the current ones are multiplied.  X fragments use the
-//   same k-slot mapping and come from L2 (X is at most 64 rows).
-// * The waves' fp32 partial tiles are summed in LDS in a fixed order, then the
+// * A workgroup owns one tile of 16 * NA weight rows (output columns), all
+//   M <= 16 * NB token rows, and one of `k_splits` slices of K; its WAVES
+//   waves split that slice further.  A wave walks its k range in 128-k steps:
+//   a lane loads 64 contiguous bytes of a weight row, which is exactly its
+//   A-operand fragment of v_mfma_f32_16x16x32_bf16 (lane (r, g) holds
+//   W[row r][k + 32g .. 32g + 31], i.e. four MFMA k-steps), and the X
+//   fragments with the same k-slot mapping (X is at most 64 rows and stays in
+//   L2).  Step i + 1's W and X are in flight while step i is multiplied; there
+//   are no dependent loads in the loop, so the in-order vmcnt waits only ever
+//   wait for the step being consumed.
+// * The waves' fp32 tiles are summed in LDS in a fixed order, then the
 //   epilogue runs on the finished tile:
-//     kStore   Y = bf16(acc)
-//     kSiluMul rows [0, N) are gate and [N, 2N) up (the fused gate_up weight,
-//              language.py:238): Y = bf16(bf16(silu(bf16(g))) * bf16(u))
-//              (the reference's bf16 rounding points, language.py:102-104)
-//     kArgmax  per token the largest bf16-rounded logit of the tile, lowest
-//              column on ties, as a 64-bit key for a later cross-tile max;
-//              optionally also stores the bf16 logits.
-//     kAddResidual  R = bf16(bf16(acc) + R): the residual add of
-//              _add_rms_norm (language.py:94-99), in place on R.
+//     kStore        Y = bf16(acc)
+//     kSiluMul      rows [0, N) are gate and [N, 2N) up (the fused gate_up
+//                   weight, language.py:238): Y = bf16(bf16(silu(bf16(g))) * bf16(u))
+//                   (the reference's rounding points, language.py:102-104)
+//     kArgmax       per token the largest bf16-rounded logit of the tile,
+//                   lowest column on ties, as a 64-bit key for a later
+//                   cross-tile max; optionally also stores the bf16 logits
+//     kAddResidual  R = bf16(bf16(acc) + R) in place: the residual add of
+//                   _add_rms_norm (language.py:94-99)
+//     kPartial      fp32 partial sums of k-slice blockIdx.y, for weights too
+//                   narrow to fill the chip with whole-K tiles; the
+//                   add + RMSNorm that follows sums them (csrc/norm.hip), so
+//                   no workgroup ever waits for another.
 // C layout: lane (l % 16, g) holds rows 4g..4g+3 of the tile for token l % 16.
 #include "common.h"
 
 namespace oxr {
 namespace {
 
-enum Epilogue { kStore = 0, kSiluMul = 1, kArgmax = 2, kAddResidual = 3 };
+enum Epilogue { kStore = 0, kSiluMul = 1, kArgmax = 2, kAddResidual = 3, kPartial = 4 };
 
-constexpr int kKStep = 128;  // k per prefetch stage: 4 MFMA k-steps of 32
+constexpr int kKStep = 128;  // k per pipeline stage: 4 MFMA k-steps of 32
 
 // Order-preserving key of a bf16 logit (as fp32 bits) and its column: larger
 // value wins, then lower column.  NaN sorts above everything (torch argmax
@@ -61,20 +68,28 @@ struct GemmArgs {
   bf16_t* y;        // kStore / kSiluMul: [M, ldy]; kArgmax: optional logits [M, ldy]; kAddResidual: R [M, ldy]
   int64_t ldy;
   uint64_t* best;   // kArgmax: [num_tiles, M]
+  float* part;      // kPartial: [k_splits, M, N]
 };
 
-template <int NA, int NB, int EPI, int KSPLIT>
-__global__ __launch_bounds__(64 * KSPLIT) void gemm_kernel(GemmArgs args) {
-  constexpr int kTileRows = 16 * NA;            // output columns of this workgroup
+template <int NT, int NB>
+struct Stage {
+  u32x4 w[NT][4];
+  u32x4 x[NB][4];
+};
+
+template <int NA, int NB, int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
+  constexpr int kTileRows = 16 * NA;                          // output columns of this workgroup
   constexpr int kLoadTiles = (EPI == kSiluMul) ? 2 * NA : NA;  // gate + up tiles for kSiluMul
-  __shared__ f32x4 red[KSPLIT > 1 ? KSPLIT - 1 : 1][KSPLIT > 1 ? kLoadTiles * NB : 1][KSPLIT > 1 ? 64 : 1];
+  __shared__ f32x4 red[WAVES > 1 ? WAVES - 1 : 1][WAVES > 1 ? kLoadTiles * NB : 1][WAVES > 1 ? 64 : 1];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * kTileRows;
   const int64_t K = args.K;
-  const int64_t k_per_wave = K / KSPLIT;
-  const int64_t k_begin = wave * k_per_wave, k_end = k_begin + k_per_wave;
+  const int64_t k_slice = K / gridDim.y;
+  const int64_t k_per_wave = k_slice / WAVES;
+  const int64_t k_begin = blockIdx.y * k_slice + wave * k_per_wave, k_end = k_begin + k_per_wave;
 
   // Weight row pointers of this lane, one per loaded tile (rows past N clamp
   // to the last row; their results are dropped).
@@ -86,13 +101,12 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_kernel(GemmArgs args) {
     if (EPI == kSiluMul && a >= NA) row += args.N;
     wrow[a] = args.w + row * K + 32 * g;
   }
+  // Token rows past M read row 0 and multiply into accumulators nobody stores.
   const bf16_t* xrow[NB];
-  bool xvalid[NB];
 #pragma unroll
   for (int bt = 0; bt < NB; ++bt) {
     const int tok = 16 * bt + r;
-    xvalid[bt] = tok < args.M;
-    xrow[bt] = args.x + (int64_t)(xvalid[bt] ? tok : 0) * args.ldx + 32 * g;
+    xrow[bt] = args.x + (int64_t)(tok < args.M ? tok : 0) * args.ldx + 32 * g;
   }
 
   f32x4 acc[kLoadTiles][NB];
@@ -101,39 +115,32 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_kernel(GemmArgs args) {
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt) acc[a][bt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 wa[kLoadTiles][4], wn[kLoadTiles][4];
+  auto load = [&](Stage<kLoadTiles, NB>& st, int64_t k) {
 #pragma unroll
-  for (int a = 0; a < kLoadTiles; ++a)
+    for (int a = 0; a < kLoadTiles; ++a)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wa[a][i] = ld128_nt(wrow[a] + k_begin + 8 * i);
+      for (int i = 0; i < 4; ++i) st.w[a][i] = ld128(wrow[a] + k + 8 * i);
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.x[bt][i] = ld128(xrow[bt] + k + 8 * i);
+  };
 
+  Stage<kLoadTiles, NB> cur, nxt;
+  load(cur, k_begin);
   for (int64_t k = k_begin; k < k_end; k += kKStep) {
     const bool more = k + kKStep < k_end;
-    if (more) {
+    if (more) load(nxt, k + kKStep);
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
       for (int a = 0; a < kLoadTiles; ++a)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) wn[a][i] = ld128_nt(wrow[a] + k + kKStep + 8 * i);
-    }
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt) {
-      u32x4 xb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xb[i] = xvalid[bt] ? ld128(xrow[bt] + k + 8 * i) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int a = 0; a < kLoadTiles; ++a)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[a][bt] = mfma_16x16x32(wa[a][i], xb[i], acc[a][bt]);
-    }
-    if (more) {
-#pragma unroll
-      for (int a = 0; a < kLoadTiles; ++a)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wa[a][i] = wn[a][i];
-    }
+        for (int i = 0; i < 4; ++i) acc[a][bt] = mfma_16x16x32(cur.w[a][i], cur.x[bt][i], acc[a][bt]);
+    if (more) cur = nxt;
   }
 
-  if constexpr (KSPLIT > 1) {
+  if constexpr (WAVES > 1) {
     if (wave > 0) {
 #pragma unroll
       for (int a = 0; a < kLoadTiles; ++a)
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_kernel(GemmArgs args) {
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
-    for (int w = 0; w < KSPLIT - 1; ++w)
+    for (int w = 0; w < WAVES - 1; ++w)
 #pragma unroll
       for (int a = 0; a < kLoadTiles; ++a)
 #pragma unroll
@@ -182,6 +189,23 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_kernel(GemmArgs args) {
       o = shfl_xor_u64(best, 32);
       best = o > best ? o : best;
       if (g == 0 && tok < args.M) args.best[(int64_t)blockIdx.x * args.M + tok] = best;
+    }
+  } else if constexpr (EPI == kPartial) {
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt) {
+      const int tok = 16 * bt + r;
+      if (tok >= args.M) continue;
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        const int64_t col0 = n0 + 16 * a + 4 * g;
+        float* dst = args.part + ((int64_t)blockIdx.y * args.M + tok) * args.N + col0;
+        if (col0 + 3 < args.N) {
+          *reinterpret_cast<f32x4*>(dst) = acc[a][bt];
+        } else {
+          for (int j = 0; j < 4; ++j)
+            if (col0 + j < args.N) dst[j] = acc[a][bt][j];
+        }
+      }
     }
   } else {
 #pragma unroll
@@ -244,41 +268,62 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint64_t* __re
   }
 }
 
-template <int NA, int NB, int EPI, int KSPLIT>
-int launch_gemm(const GemmArgs& a, int64_t tiles, hipStream_t s) {
-  hipLaunchKernelGGL((gemm_kernel<NA, NB, EPI, KSPLIT>), dim3((unsigned)tiles), dim3(64 * KSPLIT), 0, s, a);
+struct LaunchConfig {
+  int na;        // 16-row tiles per workgroup
+  int waves;     // waves per workgroup, each a k sub-slice
+  int k_splits;  // k slices across workgroups (kPartial only)
+};
+
+template <int NA, int NB, int EPI, int WAVES>
+int launch_gemm(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
+  const int64_t tiles = (a.N + 16 * NA - 1) / (16 * NA);
+  hipLaunchKernelGGL((gemm_kernel<NA, NB, EPI, WAVES>), dim3((unsigned)tiles, (unsigned)c.k_splits), dim3(64 * WAVES),
+                     0, s, a);
   return OXR_LAUNCH_STATUS();
 }
 
-template <int NA, int EPI, int KSPLIT>
-int dispatch_nb(const GemmArgs& a, int64_t tiles, hipStream_t s) {
-  const int nb = (a.M + 15) / 16;
-  switch (nb) {
-    case 1: return launch_gemm<NA, 1, EPI, KSPLIT>(a, tiles, s);
-    case 2: return launch_gemm<NA, 2, EPI, KSPLIT>(a, tiles, s);
-    case 3: return launch_gemm<NA, 3, EPI, KSPLIT>(a, tiles, s);
-    case 4: return launch_gemm<NA, 4, EPI, KSPLIT>(a, tiles, s);
+template <int NA, int EPI, int WAVES>
+int dispatch_nb(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
+  switch ((a.M + 15) / 16) {
+    case 1: return launch_gemm<NA, 1, EPI, WAVES>(a, c, s);
+    case 2: return launch_gemm<NA, 2, EPI, WAVES>(a, c, s);
+    case 3: return launch_gemm<NA, 3, EPI, WAVES>(a, c, s);
+    case 4: return launch_gemm<NA, 4, EPI, WAVES>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
 template <int NA, int EPI>
-int dispatch_split(const GemmArgs& a, int64_t tiles, int ksplit, hipStream_t s) {
-  switch (ksplit) {
-    case 1: return dispatch_nb<NA, EPI, 1>(a, tiles, s);
-    case 2: return dispatch_nb<NA, EPI, 2>(a, tiles, s);
-    case 4: return dispatch_nb<NA, EPI, 4>(a, tiles, s);
-    case 8: return dispatch_nb<NA, EPI, 8>(a, tiles, s);
+int dispatch_waves(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
+  switch (c.waves) {
+    case 1: return dispatch_nb<NA, EPI, 1>(a, c, s);
+    case 2: return dispatch_nb<NA, EPI, 2>(a, c, s);
+    case 4: return dispatch_nb<NA, EPI, 4>(a, c, s);
+    case 8: return dispatch_nb<NA, EPI, 8>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
-// Waves per workgroup: enough workgroups and waves to keep every CU
-// streaming, with at least one 128-k stage per wave.
-int choose_split(int64_t tiles, int64_t K) {
-  int split = 1;
-  while (split < 8 && tiles * split < 1024 && (K / (split * 2)) % kKStep == 0 && K / (split * 2) >= kKStep) split *= 2;
-  return split;
+template <int EPI>
+int dispatch(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
+  switch (c.na) {
+    case 1: return dispatch_waves<1, EPI>(a, c, s);
+    case 2: return dispatch_waves<2, EPI>(a, c, s);
+    default: return OXR_ERR_UNSUPPORTED;
+  }
+}
+
+// Launch shape: about 2048 waves (8 per CU) in all, each with at least one
+// 128-k stage; k is split across workgroups only when the caller takes fp32
+// partials and there are too few row tiles to give every CU a workgroup.
+LaunchConfig choose_config(int64_t n_rows, int64_t K, int na, bool allow_k_splits) {
+  LaunchConfig c{na, 1, 1};
+  const int64_t tiles = (n_rows + 16 * na - 1) / (16 * na);
+  if (allow_k_splits)
+    while (tiles * c.k_splits < 256 && K % (2 * c.k_splits * kKStep) == 0 && c.k_splits < 16) c.k_splits *= 2;
+  const int64_t k_slice = K / c.k_splits;
+  while (c.waves < 8 && tiles * c.k_splits * c.waves < 2048 && k_slice % (2 * c.waves * kKStep) == 0) c.waves *= 2;
+  return c;
 }
 
 int check_common(const void* x, int64_t ldx, int64_t M, const void* w, int64_t K, int64_t N) {
@@ -300,15 +345,29 @@ extern "C" int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const ox
   OXR_RETURN_IF(epilogue != kStore && epilogue != kSiluMul && epilogue != kAddResidual, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(!y || ldy < n || ldy % 4 != 0 || (uintptr_t)y % 8 != 0, OXR_ERR_INVALID_ARG);
   if (m == 0) return OXR_OK;
-  GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, nullptr};
+  GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
-  if (epilogue == kSiluMul) {
-    const int64_t tiles = (n + 15) / 16;
-    return dispatch_split<1, kSiluMul>(a, tiles, choose_split(tiles, k), s);
-  }
-  const int64_t tiles = (n + 15) / 16;
-  if (epilogue == kAddResidual) return dispatch_split<1, kAddResidual>(a, tiles, choose_split(tiles, k), s);
-  return dispatch_split<1, kStore>(a, tiles, choose_split(tiles, k), s);
+  const LaunchConfig c = choose_config(n, k, 1, false);
+  if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, s);
+  if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, s);
+  return dispatch<kStore>(a, c, s);
+}
+
+extern "C" int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k) {
+  return oxr::choose_config(n, k, 1, true).k_splits;
+}
+
+extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k,
+                                     int64_t n, float* partials, int32_t k_splits, oxr_stream_t stream) {
+  using namespace oxr;
+  int st = check_common(x, ldx, m, w, k, n);
+  if (st) return st;
+  OXR_RETURN_IF(!partials || (uintptr_t)partials % 16 != 0 || n % 4 != 0, OXR_ERR_INVALID_ARG);
+  const LaunchConfig c = choose_config(n, k, 1, true);
+  OXR_RETURN_IF(k_splits != c.k_splits, OXR_ERR_INVALID_ARG);
+  if (m == 0) return OXR_OK;
+  GemmArgs a{x, ldx, (int)m, w, k, n, nullptr, 0, nullptr, partials};
+  return dispatch<kPartial>(a, c, (hipStream_t)stream);
 }
 
 extern "C" size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab) {
@@ -329,9 +388,11 @@ extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_b
   const size_t need = oxr_lm_head_workspace_bytes(m, vocab);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
   const int64_t tiles = (vocab + 31) / 32;
-  GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, static_cast<uint64_t*>(workspace)};
+  GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab,
+             static_cast<uint64_t*>(workspace), nullptr};
   hipStream_t s = (hipStream_t)stream;
-  st = dispatch_split<2, kArgmax>(a, tiles, 1, s);
+  const LaunchConfig c = choose_config(vocab, hidden_size, 2, false);
+  st = dispatch<kArgmax>(a, c, s);
   if (st) return st;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(workspace),
                      (int)tiles, (int)m, predicted);

@@ -8,10 +8,10 @@
 //   var = sum(h^2) / D            (fp32; one wave per row, lane-local sums of
 //                                   D/64 values then a butterfly across lanes)
 //   out = bf16(w * bf16(h * (1 / sqrt(var + eps))))
-// The residual add that precedes the norm in _add_rms_norm is fused into the
-// GEMM that produces its input (csrc/gemm.hip), so this kernel only
-// normalises.  With kEmbed the row is gathered from the embedding table by
-// token id and also stored as the new residual stream.
+// Three sources for the row: a plain row (kRows); the embedding table row of
+// a token id, also stored as the new residual stream (kEmbed); or the residual
+// add of _add_rms_norm with the preceding GEMM's fp32 k-split partials summed
+// here (kAddPartials), so the GEMM needs no cross-workgroup reduction.
 #include "common.h"
 
 namespace oxr {
@@ -19,9 +19,17 @@ namespace {
 
 constexpr int kMaxVec = 8;  // up to 8 x 16 B per lane: D <= 4096
 
-template <bool kEmbed, int VEC>
+enum Source { kRows = 0, kEmbed = 1, kAddPartials = 2 };
+
+// MODE kRows: x is [rows, ldx].  kEmbed: row = table[ids[row]], also stored as
+// the residual.  kAddPartials: row = bf16(bf16(sum of the k-split fp32
+// partials of the GEMM that produced it) + residual), stored back as the
+// residual (the add of _add_rms_norm, language.py:94-99, with the GEMM's
+// bf16 output rounding first, as the reference's nn.Linear does).
+template <int MODE, int VEC>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
-                                                       const int64_t* __restrict__ ids, int64_t vocab, int rows,
+                                                       const int64_t* __restrict__ ids, int64_t vocab,
+                                                       const float* __restrict__ partials, int k_splits, int rows,
                                                        int D, const bf16_t* __restrict__ w, float eps,
                                                        bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
                                                        int64_t ldo) {
@@ -29,10 +37,12 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t* __restrict_
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
   const bf16_t* src;
-  if constexpr (kEmbed) {
+  if constexpr (MODE == kEmbed) {
     int64_t id = ids[row];
     id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // stay inside the table
     src = x + id * ldx;
+  } else if constexpr (MODE == kAddPartials) {
+    src = residual + (int64_t)row * ldo;
   } else {
     src = x + (int64_t)row * ldx;
   }
@@ -40,7 +50,23 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t* __restrict_
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
-    v[i] = ld128(src + (i * kWave + lane) * 8);
+    const int col = (i * kWave + lane) * 8;
+    v[i] = ld128(src + col);
+    if constexpr (MODE == kAddPartials) {
+      f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < k_splits; ++sp) {
+        const float* p = partials + ((int64_t)sp * rows + row) * D + col;
+        lo += *reinterpret_cast<const f32x4*>(p);
+        hi += *reinterpret_cast<const f32x4*>(p + 4);
+      }
+      const uint32_t rd[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      const float sum[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = pack_bf(round_bf16(sum[2 * e]) + lo_bf(rd[e]), round_bf16(sum[2 * e + 1]) + hi_bf(rd[e]));
+      v[i] = u32x4{o[0], o[1], o[2], o[3]};
+    }
     const uint32_t wd[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -66,19 +92,19 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t* __restrict_
       o[e] = pack_bf(y0, y1);
     }
     st128(out + (int64_t)row * ldo + col, u32x4{o[0], o[1], o[2], o[3]});
-    if constexpr (kEmbed) st128(residual + (int64_t)row * ldo + col, v[i]);
+    if constexpr (MODE != kRows) st128(residual + (int64_t)row * ldo + col, v[i]);
   }
 }
 
-template <bool kEmbed>
-int launch(const bf16_t* x, int64_t ldx, const int64_t* ids, int64_t vocab, int rows, int D, const bf16_t* w,
-           float eps, bf16_t* residual, bf16_t* out, int64_t ldo, hipStream_t s) {
+template <int MODE>
+int launch(const bf16_t* x, int64_t ldx, const int64_t* ids, int64_t vocab, const float* partials, int k_splits,
+           int rows, int D, const bf16_t* w, float eps, bf16_t* residual, bf16_t* out, int64_t ldo, hipStream_t s) {
   const dim3 grid((rows + 3) / 4), block(256);
   switch (D / (kWave * 8)) {
-#define OXR_CASE(n)                                                                                                \
-  case n:                                                                                                          \
-    hipLaunchKernelGGL((rms_norm_kernel<kEmbed, n>), grid, block, 0, s, x, ldx, ids, vocab, rows, D, w, eps, residual, \
-                       out, ldo);                                                                                  \
+#define OXR_CASE(n)                                                                                               \
+  case n:                                                                                                         \
+    hipLaunchKernelGGL((rms_norm_kernel<MODE, n>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, \
+                       D, w, eps, residual, out, ldo);                                                            \
     break;
     OXR_CASE(1) OXR_CASE(2) OXR_CASE(3) OXR_CASE(4) OXR_CASE(5) OXR_CASE(6) OXR_CASE(7) OXR_CASE(8)
 #undef OXR_CASE
@@ -105,7 +131,7 @@ extern "C" int oxr_rms_norm(const oxr_bf16* x, int64_t ldx, int64_t rows, int64_
   if (st) return st;
   if (rows == 0) return OXR_OK;
   OXR_RETURN_IF(!x || !weight || !out, OXR_ERR_INVALID_ARG);
-  return launch<false>(x, ldx, nullptr, 0, (int)rows, (int)hidden, weight, eps, nullptr, out, ldo,
+  return launch<kRows>(x, ldx, nullptr, 0, nullptr, 0, (int)rows, (int)hidden, weight, eps, nullptr, out, ldo,
                        (hipStream_t)stream);
 }
 
@@ -117,6 +143,19 @@ extern "C" int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf
   if (st) return st;
   if (rows == 0) return OXR_OK;
   OXR_RETURN_IF(!ids || !table || vocab <= 0 || !weight || !residual || !out, OXR_ERR_INVALID_ARG);
-  return launch<true>(table, hidden, ids, vocab, (int)rows, (int)hidden, weight, eps, residual, out, hidden,
-                      (hipStream_t)stream);
+  return launch<kEmbed>(table, hidden, ids, vocab, nullptr, 0, (int)rows, (int)hidden, weight, eps, residual, out,
+                        hidden, (hipStream_t)stream);
+}
+
+extern "C" int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t rows, int64_t hidden,
+                                         oxr_bf16* residual, const oxr_bf16* weight, float eps, oxr_bf16* out,
+                                         oxr_stream_t stream) {
+  using namespace oxr;
+  int st = check(rows, hidden, hidden, hidden);
+  if (st) return st;
+  OXR_RETURN_IF(k_splits < 1, OXR_ERR_INVALID_ARG);
+  if (rows == 0) return OXR_OK;
+  OXR_RETURN_IF(!partials || !residual || !weight || !out, OXR_ERR_INVALID_ARG);
+  return launch<kAddPartials>(nullptr, hidden, nullptr, 0, partials, k_splits, (int)rows, (int)hidden, weight, eps,
+                              residual, out, hidden, (hipStream_t)stream);
 }

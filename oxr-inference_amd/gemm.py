@@ -6,6 +6,9 @@ These replace the ``nn.Linear`` projections of the reference decoder layer (lang
 - ``linear``            ``x @ w.T``                       (qkv_proj, o_proj, down_proj)
 - ``linear_silu_mul``   ``_silu_mul(x @ w.T)``            (gate_up_proj + SiLU*up, language.py:102-104)
 - ``linear_add_``       ``residual += x @ w.T`` in bf16   (the add of ``_add_rms_norm``, language.py:94-99)
+- ``linear_partial``    fp32 k-split partial sums of ``x @ w.T`` for weights too narrow to fill the chip
+                        (o_proj, down_proj); ``add_partials_rms_norm`` finishes the sum, the residual add
+                        and the next RMSNorm in one pass
 """
 
 from __future__ import annotations
@@ -66,3 +69,33 @@ def linear_add_(residual: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> tor
                  "linear_add_: residual must be bf16 [m, n]")
     _run(x, w, n, EPI_ADD_RESIDUAL, residual, device)
     return residual
+
+
+def partial_splits(n: int, k: int) -> int:
+    """How many k slices ``linear_partial`` uses for an ``[n, k]`` weight."""
+    return int(_lib.lib().oxr_gemm_bf16_partial_splits(n, k))
+
+
+def linear_partial(x: torch.Tensor, w: torch.Tensor, partials: torch.Tensor) -> int:
+    """fp32 partial sums of ``x @ w.T`` over ``partial_splits(n, k)`` k slices into
+    ``partials[:splits, :m, :n]``; returns the number of slices."""
+    device = _check(x, w, "linear_partial")
+    m, (n, k) = x.shape[0], w.shape
+    _lib.require(m <= MAX_ROWS, "linear_partial: at most 64 rows")
+    splits = partial_splits(n, k)
+    _lib.require(partials.dtype == torch.float32 and partials.is_contiguous() and partials.numel() >= splits * m * n,
+                 "linear_partial: partials must be contiguous fp32 with room for splits * m * n")
+    _lib.call("oxr_gemm_bf16_partial", x.data_ptr(), x.stride(0), m, w.data_ptr(), k, n, partials.data_ptr(), splits,
+              _lib.stream(device))
+    return splits
+
+
+def add_partials_rms_norm(partials: torch.Tensor, splits: int, residual: torch.Tensor, weight: torch.Tensor,
+                          eps: float, out: torch.Tensor) -> torch.Tensor:
+    """``residual = bf16(bf16(sum of partials) + residual)``; ``out = rms_norm(residual) * weight``
+    (``_add_rms_norm``, language.py:94-99, taking a ``linear_partial`` result)."""
+    device = _lib.require_gpu(partials, residual, weight, out, name="add_partials_rms_norm")
+    rows, hidden = residual.shape
+    _lib.call("oxr_add_partials_rms_norm", partials.data_ptr(), splits, rows, hidden, residual.data_ptr(),
+              weight.data_ptr(), float(eps), out.data_ptr(), _lib.stream(device))
+    return out

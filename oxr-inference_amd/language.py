@@ -7,14 +7,16 @@ Per layer (language.py:301-317 with the fused projections of :234-245):
     qkv      = h @ Wqkv^T                                       oxr_gemm_bf16
     q        = qk_norm_rope_store(qkv, ...)  (K/V -> cache)     oxr_qk_norm_rope_store_at
     attn     = paged_extend(q, cache, seq_lens, block_table)    oxr_paged_extend
-    residual = bf16(bf16(attn @ Wo^T) + residual)               oxr_gemm_bf16 (add epilogue)
-    h        = rms_norm(residual)                               oxr_rms_norm
+    o_part   = k-split fp32 sums of attn @ Wo^T                 oxr_gemm_bf16_partial
+    residual = bf16(bf16(sum o_part) + residual); h = rms_norm  oxr_add_partials_rms_norm
     act      = silu(h @ Wg^T) * (h @ Wu^T)                      oxr_gemm_bf16 (SiLU*mul epilogue)
-    residual = bf16(bf16(act @ Wd^T) + residual)                oxr_gemm_bf16 (add epilogue)
+    d_part   = k-split fp32 sums of act @ Wd^T                  oxr_gemm_bf16_partial
 
-then ``hidden = rms_norm(residual)`` and the LM head with fused argmax.  The residual adds of
-``_add_rms_norm`` (language.py:94-99) move into the GEMM epilogues; the rounding points are
-the reference's (residual stored in bf16 before it is normalised).
+and the next layer's input norm (or the final norm) starts with the residual add of d_part.
+o_proj and down_proj have only 2048 output columns: split over k so every CU streams weights,
+their partials are summed by the norm that follows, which also does ``_add_rms_norm``'s residual
+add (language.py:94-99) with the reference's rounding points (GEMM output rounded to bf16, then
+added, residual stored in bf16 before it is normalised).
 
 All intermediate buffers live in a preallocated :class:`StepBuffers`, so a forward enqueues
 kernels only and can be captured in a HIP graph.
@@ -143,9 +145,11 @@ class StepBuffers:
     attn_workspace: torch.Tensor
     head_workspace: torch.Tensor
     predicted: torch.Tensor
+    partials: torch.Tensor  # fp32 k-split sums of o_proj / down_proj, consumed by the next norm
     max_tokens: int
     max_seq_len: int
     max_batch: int = field(default=0)
+    pending_splits: int = field(default=0)  # partials not yet added to the residual (0: none)
 
     @classmethod
     def allocate(cls, config: LanguageConfig, max_batch: int, tokens_per_seq: int, max_seq_len: int,
@@ -163,6 +167,9 @@ class StepBuffers:
             head_workspace=torch.zeros(max(lm_head.workspace_bytes(t, config.vocab_size), 1), dtype=torch.uint8,
                                        device=device),
             predicted=torch.zeros(t, dtype=torch.int64, device=device),
+            partials=torch.zeros(max(gemm.partial_splits(config.hidden_size, config.num_heads * config.head_dim),
+                                     gemm.partial_splits(config.hidden_size, config.intermediate_size)),
+                                 t, config.hidden_size, dtype=torch.float32, device=device),
             max_tokens=t, max_seq_len=max_seq_len, max_batch=max_batch,
         )
 
@@ -193,6 +200,7 @@ class LanguageModel:
 
     def embed(self, batch: ExtendBatch, buffers: StepBuffers) -> None:
         """residual = embed_tokens(ids) (decode_graph.py:164); h = layer 0's input norm of it."""
+        buffers.pending_splits = 0
         c, w = self.config, self.weights
         t = batch.block_table.shape[0] * batch.tokens_per_seq
         res, h = buffers.residual[:t], buffers.h[:t]
@@ -209,10 +217,21 @@ class LanguageModel:
         _lib.call("oxr_rms_norm", x.data_ptr(), x.stride(0), x.shape[0], c.hidden_size, weight.data_ptr(),
                   float(c.rms_norm_eps), out.data_ptr(), out.stride(0), stream)
 
+    def _settle_norm(self, buffers: StepBuffers, t: int, weight: torch.Tensor, stream: int) -> None:
+        """h = rms_norm(residual) * weight, first adding any pending GEMM partials to the residual."""
+        res, h = buffers.residual[:t], buffers.h[:t]
+        if buffers.pending_splits:
+            gemm.add_partials_rms_norm(buffers.partials, buffers.pending_splits, res, weight,
+                                       self.config.rms_norm_eps, h)
+            buffers.pending_splits = 0
+        else:
+            self._norm(res, weight, h, stream)
+
     def run_layers(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers, start: int, stop: int, *,
                    first_norm_done: bool = False) -> None:
         """Layers ``[start, stop)`` on ``buffers.residual`` (the residual stream after the previous
-        layer's MLP add); afterwards it holds the residual after layer ``stop - 1``."""
+        layer's MLP add).  The last layer's down_proj is left as pending partials: the next norm
+        (``run_layers``, ``final_norm`` or ``settle``) adds it to the residual."""
         c, w = self.config, self.weights
         b, s = batch.block_table.shape[0], batch.tokens_per_seq
         t = b * s
@@ -228,7 +247,7 @@ class LanguageModel:
         for index in range(start, stop):
             layer = w.layers[index]
             if not (first_norm_done and index == start):
-                self._norm(res, layer.input_norm, h, stream)
+                self._settle_norm(buffers, t, layer.input_norm, stream)
             gemm.linear(h, layer.qkv, out=qkv)
             k_cache, v_cache = cache.k[index], cache.v[index]
             _lib.call(
@@ -239,16 +258,20 @@ class LanguageModel:
             )
             attention.paged_extend(q, k_cache, v_cache, batch.seq_lens, batch.block_table, scale=c.head_dim ** -0.5,
                                    max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace)
-            gemm.linear_add_(res, attn_flat, layer.o)
-            self._norm(res, layer.post_norm, h, stream)
+            buffers.pending_splits = gemm.linear_partial(attn_flat, layer.o, buffers.partials)
+            self._settle_norm(buffers, t, layer.post_norm, stream)
             gemm.linear_silu_mul(h, layer.gate_up, out=act)
-            gemm.linear_add_(res, act, layer.down)
+            buffers.pending_splits = gemm.linear_partial(act, layer.down, buffers.partials)
+
+    def settle(self, batch: ExtendBatch, buffers: StepBuffers, weight: torch.Tensor) -> None:
+        """Add pending partials to the residual (and normalise it with ``weight`` into ``h``)."""
+        t = batch.block_table.shape[0] * batch.tokens_per_seq
+        self._settle_norm(buffers, t, weight, _lib.stream(batch.positions.device))
 
     def final_norm(self, batch: ExtendBatch, buffers: StepBuffers) -> torch.Tensor:
         t = batch.block_table.shape[0] * batch.tokens_per_seq
-        h = buffers.h[:t]
-        self._norm(buffers.residual[:t], self.weights.final_norm, h, _lib.stream(batch.positions.device))
-        return h
+        self._settle_norm(buffers, t, self.weights.final_norm, _lib.stream(batch.positions.device))
+        return buffers.h[:t]
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         """bf16 ``hidden @ lm_head^T`` (language.py:213-214)."""

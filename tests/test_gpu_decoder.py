@@ -112,12 +112,15 @@ def test_each_layer_within_bf16_tolerance() -> None:
     slots = torch.from_numpy(batch.slots)
     for i in range(SMALL.num_layers):
         buffers.residual[:t].copy_(trace[i].cuda())
+        buffers.pending_splits = 0
         model.run_layers(eb, cache, buffers, i, i + 1)
+        model.settle(eb, buffers, cpu_w.final_norm.cuda())  # adds the layer's pending down_proj partials
         torch.cuda.synchronize()
         _residual_close(buffers.residual[:t], trace[i + 1])
         _close(flat(cache.k[i].cpu())[slots], flat(cpu_k[i])[slots])
         _close(flat(cache.v[i].cpu())[slots], flat(cpu_v[i])[slots])
     buffers.residual[:t].copy_(trace[-1].cuda())
+    buffers.pending_splits = 0
     hidden = model.final_norm(eb, buffers)
     _close(hidden, want_hidden)
     pred = model.greedy(hidden).cpu().numpy()

@@ -132,3 +132,34 @@ def test_lm_head_ties_take_lowest_index() -> None:
     torch.cuda.synchronize()
     assert int(pred[0]) == 3 and int(pred[1]) == 5
     assert np.array_equal(pred.cpu().numpy(), oracle_lm_head.argmax(_bits(logits)))
+
+
+@pytest.mark.parametrize("k", [2048, 6144])
+def test_partial_gemm_then_add_rms_norm(k: int) -> None:
+    """o_proj / down_proj path: k-split fp32 partials summed by the following add + RMSNorm:
+    residual' = bf16(bf16(x @ w.T) + residual), h = bf16(w_n * bf16(residual' * rsqrt(mean sq + eps)))."""
+    g = torch.Generator(device="cuda").manual_seed(k)
+    m, n = 32, 2048
+    x, w, r = _rand(g, m, k), _rand(g, n, k, std=0.02), _rand(g, m, n)
+    wn = (0.5 + torch.rand(n, generator=g, device="cuda")).to(torch.bfloat16)
+    r0 = _bits(r).copy()
+    splits = gemm.partial_splits(n, k)
+    assert splits >= 2
+    partials = torch.full((splits, m, n), float("nan"), device="cuda")
+    h = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    announce("partial gemm + add norm", k, splits)
+    assert gemm.linear_partial(x, w, partials) == splits
+    gemm.add_partials_rms_norm(partials, splits, r, wn, 1e-6, h)
+    torch.cuda.synchronize()
+    exact = _exact(x, w)
+    prod = bf16.round_f32(exact.astype(np.float32)).astype(np.float64)
+    want_r = bf16.round_f32((prod + bf16.to_f32(r0)).astype(np.float32)).astype(np.float64)
+    got_r = bf16.to_f32(_bits(r)).astype(np.float64)
+    assert (np.abs(got_r - want_r) <= _ulp_bf16(prod) + _ulp_bf16(want_r) + _order_slack(x, w)).all()
+    assert np.mean(got_r == want_r) > 0.98
+    # The norm of the residual actually stored (exact inputs): within the bf16 tolerance.
+    rr = got_r.astype(np.float32)
+    inv = (1.0 / np.sqrt((rr.astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-6))
+    want_h = bf16.to_f32(_bits(wn)).astype(np.float64) * bf16.round_f32((rr * inv).astype(np.float32))
+    got_h = bf16.to_f32(_bits(h)).astype(np.float64)
+    assert (np.abs(got_h - want_h) <= ATOL + RTOL * np.abs(want_h)).all()
