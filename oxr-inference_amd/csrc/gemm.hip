@@ -313,16 +313,25 @@ int dispatch(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   }
 }
 
-// Launch shape: about 2048 waves (8 per CU) in all, each with at least one
-// 128-k stage; k is split across workgroups only when the caller takes fp32
-// partials and there are too few row tiles to give every CU a workgroup.
-LaunchConfig choose_config(int64_t n_rows, int64_t K, int na, bool allow_k_splits) {
-  LaunchConfig c{na, 1, 1};
-  const int64_t tiles = (n_rows + 16 * na - 1) / (16 * na);
-  if (allow_k_splits)
+// Launch shape, from a sweep of the verify shapes on MI355X (M = 32):
+// weights with fp32-partial output (o_proj, down_proj: 2048 columns) take
+// 32-row tiles split over k until there are >= 256 workgroups of 4 waves;
+// others take 32-row tiles when that still gives >= 160 workgroups (gate_up,
+// LM head), else 16-row tiles (qkv), with 4 waves per workgroup (2 when there
+// are thousands of tiles, as in the LM head).
+LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
+  LaunchConfig c{1, 1, 1};
+  if (allow_k_splits) {
+    c.na = 2;
+    const int64_t tiles = (n_rows + 31) / 32;
     while (tiles * c.k_splits < 256 && K % (2 * c.k_splits * kKStep) == 0 && c.k_splits < 16) c.k_splits *= 2;
+  } else {
+    c.na = (n_rows + 31) / 32 >= 160 ? 2 : 1;
+  }
+  const int64_t tiles = (n_rows + 16 * c.na - 1) / (16 * c.na);
+  const int want_waves = tiles >= 2048 ? 2 : 4;
   const int64_t k_slice = K / c.k_splits;
-  while (c.waves < 8 && tiles * c.k_splits * c.waves < 2048 && k_slice % (2 * c.waves * kKStep) == 0) c.waves *= 2;
+  while (c.waves < want_waves && k_slice % (2 * c.waves * kKStep) == 0) c.waves *= 2;
   return c;
 }
 
@@ -347,14 +356,14 @@ extern "C" int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const ox
   if (m == 0) return OXR_OK;
   GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
-  const LaunchConfig c = choose_config(n, k, 1, false);
+  const LaunchConfig c = choose_config(n, k, false);
   if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, s);
   if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, s);
   return dispatch<kStore>(a, c, s);
 }
 
 extern "C" int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k) {
-  return oxr::choose_config(n, k, 1, true).k_splits;
+  return oxr::choose_config(n, k, true).k_splits;
 }
 
 extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k,
@@ -363,7 +372,7 @@ extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, 
   int st = check_common(x, ldx, m, w, k, n);
   if (st) return st;
   OXR_RETURN_IF(!partials || (uintptr_t)partials % 16 != 0 || n % 4 != 0, OXR_ERR_INVALID_ARG);
-  const LaunchConfig c = choose_config(n, k, 1, true);
+  const LaunchConfig c = choose_config(n, k, true);
   OXR_RETURN_IF(k_splits != c.k_splits, OXR_ERR_INVALID_ARG);
   if (m == 0) return OXR_OK;
   GemmArgs a{x, ldx, (int)m, w, k, n, nullptr, 0, nullptr, partials};
@@ -372,7 +381,7 @@ extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, 
 
 extern "C" size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab) {
   if (m <= 0 || vocab <= 0) return 0;
-  return (size_t)((vocab + 31) / 32) * (size_t)m * sizeof(uint64_t);
+  return (size_t)((vocab + 15) / 16) * (size_t)m * sizeof(uint64_t);  // enough for 16-row tiles
 }
 
 extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size,
@@ -387,11 +396,11 @@ extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_b
   if (m == 0) return OXR_OK;
   const size_t need = oxr_lm_head_workspace_bytes(m, vocab);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
-  const int64_t tiles = (vocab + 31) / 32;
   GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab,
              static_cast<uint64_t*>(workspace), nullptr};
   hipStream_t s = (hipStream_t)stream;
-  const LaunchConfig c = choose_config(vocab, hidden_size, 2, false);
+  const LaunchConfig c = choose_config(vocab, hidden_size, false);
+  const int64_t tiles = (vocab + 16 * c.na - 1) / (16 * c.na);
   st = dispatch<kArgmax>(a, c, s);
   if (st) return st;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(workspace),

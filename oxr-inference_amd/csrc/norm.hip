@@ -5,8 +5,8 @@
 // 253-257, 267-268), and the embedding lookup of the verify step
 // (decode_graph.py:164, embed_tokens(ids)):
 //   h   = f32(x)
-//   var = sum(h^2) / D            (fp32; one wave per row, lane-local sums of
-//                                   D/64 values then a butterfly across lanes)
+//   var = sum(h^2) / D            (fp32; per thread 8 values, then a butterfly
+//                                   across the wave and a sum over the waves)
 //   out = bf16(w * bf16(h * (1 / sqrt(var + eps))))
 // Three sources for the row: a plain row (kRows); the embedding table row of
 // a token id, also stored as the new residual stream (kEmbed); or the residual
@@ -17,25 +17,29 @@
 namespace oxr {
 namespace {
 
-constexpr int kMaxVec = 8;  // up to 8 x 16 B per lane: D <= 4096
+constexpr int kMaxThreads = 512;  // one 8-element vector per thread: D <= 4096
 
 enum Source { kRows = 0, kEmbed = 1, kAddPartials = 2 };
 
-// MODE kRows: x is [rows, ldx].  kEmbed: row = table[ids[row]], also stored as
-// the residual.  kAddPartials: row = bf16(bf16(sum of the k-split fp32
-// partials of the GEMM that produced it) + residual), stored back as the
-// residual (the add of _add_rms_norm, language.py:94-99, with the GEMM's
-// bf16 output rounding first, as the reference's nn.Linear does).
-template <int MODE, int VEC>
-__global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
-                                                       const int64_t* __restrict__ ids, int64_t vocab,
-                                                       const float* __restrict__ partials, int k_splits, int rows,
-                                                       int D, const bf16_t* __restrict__ w, float eps,
-                                                       bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
-                                                       int64_t ldo) {
-  const int row = blockIdx.x * 4 + threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  if (row >= rows) return;
+// One workgroup per row, one 16-byte vector (8 elements) per thread, so a row
+// is read in one round of loads by D/8 threads across the CUs, and the norm
+// weights are fetched at the same time.  MODE kRows: x is [rows, ldx].
+// kEmbed: row = table[ids[row]], also stored as the residual.  kAddPartials:
+// row = bf16(bf16(sum of the k-split fp32 partials of the GEMM that produced
+// it) + residual), stored back as the residual (the add of _add_rms_norm,
+// language.py:94-99, with the GEMM's bf16 output rounding first, as the
+// reference's nn.Linear does).
+template <int MODE, int SPLITS>
+__global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
+                                                               const int64_t* __restrict__ ids, int64_t vocab,
+                                                               const float* __restrict__ partials, int k_splits,
+                                                               int rows, int D, const bf16_t* __restrict__ w, float eps,
+                                                               bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
+                                                               int64_t ldo) {
+  __shared__ float wave_ss[kMaxThreads / kWave];
+  const int row = blockIdx.x;
+  const int col = threadIdx.x * 8;
+  const u32x4 wt = ld128(w + col);
   const bf16_t* src;
   if constexpr (MODE == kEmbed) {
     int64_t id = ids[row];
@@ -46,78 +50,71 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t* __restrict_
   } else {
     src = x + (int64_t)row * ldx;
   }
-  u32x4 v[VEC];
+  u32x4 v = ld128(src + col);
+  if constexpr (MODE == kAddPartials) {
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+    const int n = SPLITS > 0 ? SPLITS : k_splits;
+#pragma unroll
+    for (int sp = 0; sp < n; ++sp) {
+      const float* p = partials + ((int64_t)sp * rows + row) * D + col;
+      lo += *reinterpret_cast<const f32x4*>(p);
+      hi += *reinterpret_cast<const f32x4*>(p + 4);
+    }
+    const uint32_t rd[4] = {v.x, v.y, v.z, v.w};
+    const float sum[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_bf(round_bf16(sum[2 * e]) + lo_bf(rd[e]), round_bf16(sum[2 * e + 1]) + hi_bf(rd[e]));
+    v = u32x4{o[0], o[1], o[2], o[3]};
+  }
+  const uint32_t xd[4] = {v.x, v.y, v.z, v.w};
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const int col = (i * kWave + lane) * 8;
-    v[i] = ld128(src + col);
-    if constexpr (MODE == kAddPartials) {
-      f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < k_splits; ++sp) {
-        const float* p = partials + ((int64_t)sp * rows + row) * D + col;
-        lo += *reinterpret_cast<const f32x4*>(p);
-        hi += *reinterpret_cast<const f32x4*>(p + 4);
-      }
-      const uint32_t rd[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-      const float sum[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf(round_bf16(sum[2 * e]) + lo_bf(rd[e]), round_bf16(sum[2 * e + 1]) + hi_bf(rd[e]));
-      v[i] = u32x4{o[0], o[1], o[2], o[3]};
-    }
-    const uint32_t wd[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = lo_bf(wd[e]), b = hi_bf(wd[e]);
-      ss += a * a;
-      ss += b * b;
-    }
+  for (int e = 0; e < 4; ++e) {
+    const float a = lo_bf(xd[e]), b = hi_bf(xd[e]);
+    ss += a * a;
+    ss += b * b;
   }
 #pragma unroll
   for (int m = 1; m < kWave; m <<= 1) ss += shfl_xor_f(ss, m);
+  if (threadIdx.x % kWave == 0) wave_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = 0.f;
+  for (int i = 0; i < (int)(blockDim.x / kWave); ++i) ss += wave_ss[i];
   const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  const uint32_t wd[4] = {wt.x, wt.y, wt.z, wt.w};
+  uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const int col = (i * kWave + lane) * 8;
-    const u32x4 wt = ld128(w + col);
-    const uint32_t xd[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-    const uint32_t wd[4] = {wt.x, wt.y, wt.z, wt.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float y0 = lo_bf(wd[e]) * round_bf16(lo_bf(xd[e]) * r);
-      const float y1 = hi_bf(wd[e]) * round_bf16(hi_bf(xd[e]) * r);
-      o[e] = pack_bf(y0, y1);
-    }
-    st128(out + (int64_t)row * ldo + col, u32x4{o[0], o[1], o[2], o[3]});
-    if constexpr (MODE != kRows) st128(residual + (int64_t)row * ldo + col, v[i]);
+  for (int e = 0; e < 4; ++e) {
+    const float y0 = lo_bf(wd[e]) * round_bf16(lo_bf(xd[e]) * r);
+    const float y1 = hi_bf(wd[e]) * round_bf16(hi_bf(xd[e]) * r);
+    o[e] = pack_bf(y0, y1);
   }
+  st128(out + (int64_t)row * ldo + col, u32x4{o[0], o[1], o[2], o[3]});
+  if constexpr (MODE != kRows) st128(residual + (int64_t)row * ldo + col, v);
 }
 
 template <int MODE>
 int launch(const bf16_t* x, int64_t ldx, const int64_t* ids, int64_t vocab, const float* partials, int k_splits,
            int rows, int D, const bf16_t* w, float eps, bf16_t* residual, bf16_t* out, int64_t ldo, hipStream_t s) {
-  const dim3 grid((rows + 3) / 4), block(256);
-  switch (D / (kWave * 8)) {
-#define OXR_CASE(n)                                                                                               \
-  case n:                                                                                                         \
-    hipLaunchKernelGGL((rms_norm_kernel<MODE, n>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, \
-                       D, w, eps, residual, out, ldo);                                                            \
-    break;
-    OXR_CASE(1) OXR_CASE(2) OXR_CASE(3) OXR_CASE(4) OXR_CASE(5) OXR_CASE(6) OXR_CASE(7) OXR_CASE(8)
-#undef OXR_CASE
-    default:
-      return OXR_ERR_UNSUPPORTED;
-  }
+  const dim3 grid(rows), block(D / 8);
+  if (MODE == kAddPartials && k_splits == 2)
+    hipLaunchKernelGGL((rms_norm_kernel<MODE, 2>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
+                       w, eps, residual, out, ldo);
+  else if (MODE == kAddPartials && k_splits == 4)
+    hipLaunchKernelGGL((rms_norm_kernel<MODE, 4>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
+                       w, eps, residual, out, ldo);
+  else
+    hipLaunchKernelGGL((rms_norm_kernel<MODE, 0>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
+                       w, eps, residual, out, ldo);
   return OXR_LAUNCH_STATUS();
 }
 
 int check(int64_t rows, int64_t D, int64_t ld, int64_t ldo) {
   OXR_RETURN_IF(rows < 0 || D <= 0 || ld < D || ldo < D, OXR_ERR_INVALID_ARG);
-  OXR_RETURN_IF(D % (kWave * 8) != 0 || D > kWave * 8 * kMaxVec || ld % 8 != 0 || ldo % 8 != 0, OXR_ERR_UNSUPPORTED);
-  OXR_RETURN_IF(rows > 0x7fffffff - 3, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(D % (kWave * 8) != 0 || D > kMaxThreads * 8 || ld % 8 != 0 || ldo % 8 != 0, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(rows > 0x7fffffff, OXR_ERR_UNSUPPORTED);
   return OXR_OK;
 }
 
