@@ -41,6 +41,22 @@ __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w <<
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ uint32_t pack_bf(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
+// Hardware round-to-nearest-even pack of two fp32 values (v_cvt_pk_bf16_f32).
+// Same bits as pack_bf for every non-NaN input; a NaN keeps its own payload
+// instead of becoming 0x7FC0, so use it only where NaN cannot occur or its
+// bits do not matter.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf_hw(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+
+// Upper 16 bits of two 32-bit words, packed lo | hi << 16 (one v_perm_b32):
+// the bf16 value of an fp32 that holds an exact bf16.
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
 // ---------------------------------------------------------------------------
 // Wave-level helpers.
 // ---------------------------------------------------------------------------

@@ -30,6 +30,8 @@
 //                   add + RMSNorm that follows sums them (csrc/norm.hip), so
 //                   no workgroup ever waits for another.
 // C layout: lane (l % 16, g) holds rows 4g..4g+3 of the tile for token l % 16.
+#include <algorithm>
+
 #include "common.h"
 
 namespace oxr {
@@ -126,18 +128,45 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
       for (int i = 0; i < 4; ++i) st.x[bt][i] = ld128(xrow[bt] + k + 8 * i);
   };
 
-  Stage<kLoadTiles, NB> cur, nxt;
-  load(cur, k_begin);
-  for (int64_t k = k_begin; k < k_end; k += kKStep) {
-    const bool more = k + kKStep < k_end;
-    if (more) load(nxt, k + kKStep);
+  auto compute = [&](const Stage<kLoadTiles, NB>& st) {
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
       for (int a = 0; a < kLoadTiles; ++a)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[a][bt] = mfma_16x16x32(cur.w[a][i], cur.x[bt][i], acc[a][bt]);
-    if (more) cur = nxt;
+        for (int i = 0; i < 4; ++i) acc[a][bt] = mfma_16x16x32(st.w[a][i], st.x[bt][i], acc[a][bt]);
+  };
+
+  // Two stages, A and B, alternate without register copies, and every load in
+  // the loop is unconditional, so the vmcnt wait before each multiply leaves
+  // the other stage's loads in flight (a conditional load, or a copy of a
+  // stage still being loaded, would make the compiler wait for everything).
+  // The last one or two steps are peeled off.  The scheduling barriers keep
+  // the loads ahead of the multiplies that they overlap.
+  const int steps = (int)(k_per_wave / kKStep);
+  Stage<kLoadTiles, NB> sa, sb;
+  load(sa, k_begin);
+  __builtin_amdgcn_sched_barrier(0);
+  int i = 0;
+  for (; i + 2 < steps; i += 2) {
+    const int64_t k = k_begin + (int64_t)i * kKStep;
+    load(sb, k + kKStep);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sa);
+    __builtin_amdgcn_sched_barrier(0);
+    load(sa, k + 2 * kKStep);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sb);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (i + 1 < steps) {
+    load(sb, k_begin + (int64_t)(i + 1) * kKStep);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sa);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sb);
+  } else {
+    compute(sa);
   }
 
   if constexpr (WAVES > 1) {
@@ -265,6 +294,191 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint64_t* __re
     for (int w = 1; w < 256 / kWave; ++w) b = part[w] > b ? part[w] : b;
     b = part[0] > b ? part[0] : b;
     predicted[m] = (int64_t)(uint32_t)(~(uint32_t)b);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Persistent LM head for M <= 32 token rows.  Every weight byte is read once,
+// so the kernel is bound by the rate at which the CUs' vector memory path
+// returns data -- and a per-wave copy of the token rows X would cost as much
+// of that path as the weights themselves (the tile kernel above loads X once
+// per wave).  Here one workgroup per CU stages all of X in LDS once, in MFMA
+// fragment order, and its 8 waves stream 16-row weight tiles through a
+// kLmDepth-stage register ring, reading X fragments from LDS.  Each wave keeps
+// a running best key per token across its tiles; the workgroup writes one key
+// per token, reduced across workgroups by argmax_reduce_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kLmWaves = 8;
+constexpr int kLmDepth = 4;          // weight stages in flight per wave
+constexpr int kLmMaxK = 2048;        // X in LDS: NB * 16 * K * 2 bytes <= 128 KB
+constexpr int kLmStageThreads = 64 * kLmWaves;
+
+template <int NB, int K>
+__global__ __launch_bounds__(64 * kLmWaves) void lm_head_lds_kernel(const bf16_t* __restrict__ x, int64_t ldx, int M,
+                                                                   const bf16_t* w, int64_t N,
+                                                                   bf16_t* __restrict__ logits, int64_t ldl,
+                                                                   uint64_t* __restrict__ best_out) {
+  static_assert(K % (kKStep * kLmDepth) == 0 && K <= kLmMaxK, "unsupported hidden size");
+  // xs[((q * 4 + i) * NB + bt) * 64 + lane] = X[16 bt + lane % 16][128 q + 32 (lane / 16) + 8 i, +8): the B
+  // fragment of MFMA i of k-stage q for token tile bt, matching the weight fragments' k-slot mapping.
+  extern __shared__ u32x4 xs[];
+  __shared__ uint64_t wave_best[kLmWaves][NB * 16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  constexpr int ksteps = K / kKStep;
+  const int64_t num_tiles = (N + 15) / 16;
+  const int64_t gw = (int64_t)blockIdx.x * kLmWaves + wave, nw = (int64_t)gridDim.x * kLmWaves;
+  const int64_t my_tiles = gw < num_tiles ? (num_tiles - 1 - gw) / nw + 1 : 0;
+  const int64_t total = my_tiles * ksteps;  // weight stages of this wave, in (tile, q) order
+
+  // Stage s of this wave: tile gw + (s / ksteps) * nw, k-stage s % ksteps.  Past the end it re-reads the
+  // last stage (an L2 hit), so every load in the loop is unconditional and the vmcnt waits are exact.
+  auto stage_ptr = [&](int64_t s) {
+    s = s < total ? s : total - 1;
+    s = s > 0 ? s : 0;  // a wave without tiles reads (and never uses) the last weight row
+    int64_t row = (gw + (s / ksteps) * nw) * 16 + r;
+    row = row < N ? row : N - 1;
+    return w + row * K + (s % ksteps) * kKStep + 32 * g;
+  };
+  auto load = [&](u32x4 (&dst)[4], int64_t s) {
+    const bf16_t* p = stage_ptr(s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = ld128(p + 8 * i);
+  };
+
+  // 1. X rows into registers (unconditional: indices past the end re-read the last chunk), then the first
+  //    weight stages, then X into LDS -- the LDS writes wait only for the X loads.
+  constexpr int kChunks = NB * 16 * (K / 8) / kLmStageThreads;  // 16-byte pieces of X per thread
+  static_assert(NB * 16 * (K / 8) % kLmStageThreads == 0, "X staging must divide evenly");
+  u32x4 xr[kChunks];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int idx = threadIdx.x + c * kLmStageThreads;
+    const int m = idx / (K / 8), k = (idx % (K / 8)) * 8;
+    xr[c] = ld128(x + (int64_t)(m < M ? m : M - 1) * ldx + k);  // rows past M: results never read
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 ring[kLmDepth][4];
+#pragma unroll
+  for (int d = 0; d < kLmDepth; ++d) load(ring[d], d);
+  // Keep these loads here, in flight during the LDS writes and the barrier
+  // (the compiler would otherwise sink them to their first use).
+  __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int idx = threadIdx.x + c * kLmStageThreads;
+    const int m = idx / (K / 8), k = (idx % (K / 8)) * 8;
+    const int q = k / kKStep, kk = k % kKStep, gg = kk / 32, ii = (kk % 32) / 8;
+    xs[((q * 4 + ii) * NB + m / 16) * 64 + gg * 16 + (m % 16)] = xr[c];
+  }
+  __syncthreads();
+
+  uint64_t best[NB];
+  f32x4 acc[NB];
+#pragma unroll
+  for (int bt = 0; bt < NB; ++bt) {
+    best[bt] = 0;
+    acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // ksteps is a multiple of kLmDepth (checked on the host), so a tile ends at d == kLmDepth - 1.
+  for (int64_t s = 0; s < total; s += kLmDepth) {
+#pragma unroll
+    for (int d = 0; d < kLmDepth; ++d) {
+      const int q = (int)((s + d) % ksteps);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int bt = 0; bt < NB; ++bt)
+          acc[bt] = mfma_16x16x32(ring[d][i], xs[((q * 4 + i) * NB + bt) * 64 + lane], acc[bt]);
+      load(ring[d], s + d + kLmDepth);
+    }
+    if ((s + kLmDepth) % ksteps == 0) {
+      const int64_t col0 = (gw + (s / ksteps) * nw) * 16 + 4 * g;
+#pragma unroll
+      for (int bt = 0; bt < NB; ++bt) {
+        const int tok = 16 * bt + r;
+        uint32_t b16[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          b16[j] = f2bf(acc[bt][j]);
+          if (col0 + j < N) {
+            const uint64_t key = argmax_key(b16[j] << 16, (uint32_t)(col0 + j));
+            best[bt] = key > best[bt] ? key : best[bt];
+          }
+        }
+        if (logits && tok < M) {
+          bf16_t* dst = logits + (int64_t)tok * ldl + col0;
+          if (col0 + 3 < N) {
+            *reinterpret_cast<u32x2*>(dst) = u32x2{b16[0] | (b16[1] << 16), b16[2] | (b16[3] << 16)};
+          } else {
+            for (int j = 0; j < 4; ++j)
+              if (col0 + j < N) dst[j] = (bf16_t)b16[j];
+          }
+        }
+        acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+
+  // Best key per token: across the 4 lane groups, then the waves, then one store per workgroup.
+#pragma unroll
+  for (int bt = 0; bt < NB; ++bt) {
+    uint64_t o = shfl_xor_u64(best[bt], 16);
+    best[bt] = o > best[bt] ? o : best[bt];
+    o = shfl_xor_u64(best[bt], 32);
+    best[bt] = o > best[bt] ? o : best[bt];
+    if (g == 0) wave_best[wave][16 * bt + r] = best[bt];
+  }
+  __syncthreads();
+  if (threadIdx.x < M) {
+    uint64_t b = 0;
+#pragma unroll
+    for (int wv = 0; wv < kLmWaves; ++wv) b = wave_best[wv][threadIdx.x] > b ? wave_best[wv][threadIdx.x] : b;
+    best_out[(int64_t)blockIdx.x * M + threadIdx.x] = b;
+  }
+}
+
+// Compute units of the current device (one persistent LM-head workgroup each).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int NB, int K>
+int launch_lm_head_lds(const bf16_t* x, int64_t ldx, int M, const bf16_t* w, int64_t N, bf16_t* logits,
+                       uint64_t* best, int grid, hipStream_t s) {
+  constexpr size_t lds = (size_t)NB * 16 * K * sizeof(bf16_t);
+  static bool attr_set = false;  // per instantiation; setting it twice is harmless
+  if (!attr_set) {
+    const hipError_t e =
+        hipFuncSetAttribute((const void*)lm_head_lds_kernel<NB, K>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((lm_head_lds_kernel<NB, K>), dim3((unsigned)grid), dim3(64 * kLmWaves), lds, s, x, ldx, M, w, N,
+                     logits, N, best);
+  return OXR_LAUNCH_STATUS();
+}
+
+// Hidden sizes with a persistent LM-head instantiation (X of up to 32 rows fits LDS).
+bool lm_head_lds_supported(int64_t m, int64_t k) { return m <= 32 && (k == 512 || k == 1024 || k == 2048); }
+
+template <int NB>
+int launch_lm_head_lds_k(const bf16_t* x, int64_t ldx, int M, const bf16_t* w, int64_t K, int64_t N, bf16_t* logits,
+                         uint64_t* best, int grid, hipStream_t s) {
+  switch (K) {
+    case 512: return launch_lm_head_lds<NB, 512>(x, ldx, M, w, N, logits, best, grid, s);
+    case 1024: return launch_lm_head_lds<NB, 1024>(x, ldx, M, w, N, logits, best, grid, s);
+    case 2048: return launch_lm_head_lds<NB, 2048>(x, ldx, M, w, N, logits, best, grid, s);
+    default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
@@ -396,14 +610,24 @@ extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_b
   if (m == 0) return OXR_OK;
   const size_t need = oxr_lm_head_workspace_bytes(m, vocab);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
-  GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab,
-             static_cast<uint64_t*>(workspace), nullptr};
   hipStream_t s = (hipStream_t)stream;
-  const LaunchConfig c = choose_config(vocab, hidden_size, false);
-  const int64_t tiles = (vocab + 16 * c.na - 1) / (16 * c.na);
-  st = dispatch<kArgmax>(a, c, s);
+  uint64_t* best = static_cast<uint64_t*>(workspace);
+  int num_best;  // partial maxima per token for the final reduction
+  if (lm_head_lds_supported(m, hidden_size)) {
+    const int64_t num_tiles = (vocab + 15) / 16;
+    num_best = (int)std::min<int64_t>(device_cus(), num_tiles);
+    st = m <= 16 ? launch_lm_head_lds_k<1>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, best,
+                                           num_best, s)
+                 : launch_lm_head_lds_k<2>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, best,
+                                           num_best, s);
+  } else {
+    GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, best, nullptr};
+    const LaunchConfig c = choose_config(vocab, hidden_size, false);
+    num_best = (int)((vocab + 16 * c.na - 1) / (16 * c.na));
+    st = dispatch<kArgmax>(a, c, s);
+  }
   if (st) return st;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(workspace),
-                     (int)tiles, (int)m, predicted);
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(best),
+                     num_best, (int)m, predicted);
   return OXR_LAUNCH_STATUS();
 }

@@ -59,21 +59,21 @@ __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict
   for (int p = 0; p < 2; ++p) {
     // A 16-key tile lies inside one page (block_size >= 16, tiles aligned to
     // 16), so its page number is wave-uniform: one scalar load, whose wait
-    // (lgkmcnt) does not hold back the vector loads already in flight.
-    const int tok = t0 + 16 * p + r;
+    // (lgkmcnt) does not hold back the vector loads already in flight.  Keys
+    // past L re-read key L - 1: their probabilities are exactly 0 and the
+    // cache rows below L hold finite values, so they add nothing.
     const int tile = __builtin_amdgcn_readfirstlane(min(t0 + 16 * p, L - 1));
     int64_t blk = table_row[tile >> log2_bs];
     blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);  // never leave the pool
-    const int64_t row = ((blk << log2_bs) + (min(tok, L - 1) & ((1 << log2_bs) - 1))) * KV + kvh;
-    const bf16_t* ks = k_cache + row * kD + 32 * g;
-    const bf16_t* vs = v_cache + row * kD + 8 * g;
+    const int64_t page = (blk << log2_bs) * KV * kD;                   // wave-uniform
+    const uint32_t tok = (uint32_t)min(t0 + 16 * p + r, L - 1);
+    const uint32_t off = ((tok & ((1u << log2_bs) - 1)) * (uint32_t)KV + (uint32_t)kvh) * kD;
+    const bf16_t* ks = k_cache + page + off + 32 * g;
+    const bf16_t* vs = v_cache + page + off + 8 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) pr.k[p][i] = ld128(ks + 8 * i);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4 x = ld128(vs + 32 * c);
-      pr.v[p][c] = tok < L ? x : u32x4{0u, 0u, 0u, 0u};  // keys past L add 0 * 0, never 0 * garbage
-    }
+    for (int c = 0; c < 4; ++c) pr.v[p][c] = ld128(vs + 32 * c);
   }
 }
 
@@ -85,11 +85,6 @@ __device__ __forceinline__ u32x4 selector(int r, int g, int shift) {
   for (int e = 0; e < 8; ++e)
     if (e == jj) w[e >> 1] |= kBf16One << (16 * (e & 1));
   return u32x4{w[0], w[1], w[2], w[3]};
-}
-
-// Upper halves (the bf16 values) of two fp32 words, packed lo | hi << 16.
-__device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
-  return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
 }
 
 constexpr int kWaves = 8;  // waves per workgroup
@@ -130,7 +125,9 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   }
   const u32x4 sel_lo = selector(r, g, 0), sel_hi = selector(r, g, 16);
 
-  float m_run = -INFINITY, l_run = 0.f;
+  // Running row maximum of the raw scores (m_run) and the same in the exp2
+  // domain (mc_run = m_run * scale * log2 e; 0 while every key is masked).
+  float m_run = -INFINITY, mc_run = 0.f, l_run = 0.f;
   f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -138,14 +135,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   // The waves take pairs wave, wave + 8, ... so at any time the workgroup reads
   // 8 neighbouring pairs of the same pages.
   const int stride = 32 * kWaves;
-  int t0 = t_begin + 32 * wave;
-  PairRegs cur, nxt;
-  if (t0 < t_end) load_pair(cur, k_cache, v_cache, table_row, t0, L, kvh, KV, log2_bs, num_blocks, r, g);
-  for (; t0 < t_end; t0 += stride) {
-    const bool more = t0 + stride < t_end;
-    if (more) load_pair(nxt, k_cache, v_cache, table_row, t0 + stride, L, kvh, KV, log2_bs, num_blocks, r, g);
-
-    // Scores of keys t0 + 16p + 4g + j for query row r.
+  auto step = [&](const PairRegs& cur, const int t0) {
+    // Raw scores of keys t0 + 16p + 4g + j for query row r.
     float sv[8];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -153,28 +144,39 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = mfma_16x16x32(cur.k[p][i], qf[i], acc);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = t0 + 16 * p + 4 * g + j;
-        sv[4 * p + j] = (tok <= qpos) ? acc[j] * scale_log2 : -INFINITY;
-      }
+      for (int j = 0; j < 4; ++j) sv[4 * p + j] = acc[j];
     }
-    float mx = sv[0];
+    if (t0 + 31 > L - S) {  // wave-uniform: only pairs at the causal frontier need the mask
 #pragma unroll
-    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+      for (int e = 0; e < 8; ++e)
+        if (t0 + 16 * (e >> 2) + 4 * g + (e & 3) > qpos) sv[e] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
     mx = fmaxf(mx, shfl_xor_f(mx, 16));
     mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;  // fully masked so far: keep p = 0
-    const float alpha = exp2f(m_run - m_use);
-    float pv[8], psum = 0.f;
+    // Probabilities exp2(s * c - m * c) against the running row maximum m;
+    // the accumulators are rescaled only when some row's maximum moved (when
+    // it did not, the factor is exactly 1).
+    const bool moved = mx > m_run;
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+      const float m_new = moved ? mx : m_run;
+      const float mc_new = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+      // (Nothing is accumulated while the maximum is -inf: factor 0, never inf.)
+      const float alpha = !moved ? 1.0f : (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc_run - mc_new));
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+      m_run = m_new;
+      mc_run = mc_new;
+    }
+    float pv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      pv[e] = exp2f(sv[e] - m_use);
-      psum += pv[e];
+      pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], scale_log2, -mc_run));
+      l_run += pv[e];
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    const u32x4 pb = {pack_bf(pv[0], pv[1]), pack_bf(pv[2], pv[3]), pack_bf(pv[4], pv[5]), pack_bf(pv[6], pv[7])};
+    const u32x4 pb = {pack_bf_hw(pv[0], pv[1]), pack_bf_hw(pv[2], pv[3]), pack_bf_hw(pv[4], pv[5]),
+                      pack_bf_hw(pv[6], pv[7])};
 
     // V^T fragments: dims 32c + [0, 16) and 32c + [16, 32) of both tiles.
 #pragma unroll
@@ -185,12 +187,34 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         const f32x4 v0 = mfma_16x16x32(cur.v[0][c], sel, z);
         const f32x4 v1 = mfma_16x16x32(cur.v[1][c], sel, z);
-        const u32x4 a = {pack_hi(v0[0], v0[1]), pack_hi(v0[2], v0[3]), pack_hi(v1[0], v1[1]), pack_hi(v1[2], v1[3])};
+        const u32x4 a = {pack_hi16(v0[0], v0[1]), pack_hi16(v0[2], v0[3]), pack_hi16(v1[0], v1[1]),
+                         pack_hi16(v1[2], v1[3])};
         const int dt = 2 * c + half;
-        o[dt] = mfma_16x16x32(a, pb, o[dt] * alpha);
+        o[dt] = mfma_16x16x32(a, pb, o[dt]);
       }
     }
-    if (more) cur = nxt;
+  };
+
+  // Two register sets, A and B, alternate without copies.  Every prefetch is
+  // issued unconditionally (past the wave's last pair it re-reads that pair,
+  // an L2 hit), so the only branch skips a compute step and the vmcnt wait
+  // before each step counts exactly the 16 loads issued after its own.
+  const int t_first = t_begin + 32 * wave;
+  const int n = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
+  if (n > 0) {
+    const int t_last = t_first + (n - 1) * stride;
+    PairRegs ra, rb;
+    load_pair(ra, k_cache, v_cache, table_row, t_first, L, kvh, KV, log2_bs, num_blocks, r, g);
+    for (int i = 0; i < n; i += 2) {
+      const int ta = t_first + i * stride;
+      load_pair(rb, k_cache, v_cache, table_row, min(ta + stride, t_last), L, kvh, KV, log2_bs, num_blocks, r, g);
+      __builtin_amdgcn_sched_barrier(0);
+      step(ra, ta);
+      load_pair(ra, k_cache, v_cache, table_row, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, num_blocks, r,
+                g);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + 1 < n) step(rb, ta + stride);
+    }
   }
 
   // Merge the 8 waves on chip.
@@ -199,7 +223,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[dt];
   if (g == 0) {
-    s_m[wave][r] = m_run;
+    s_m[wave][r] = m_run == -INFINITY ? -INFINITY : mc_run;
     s_l[wave][r] = l_tot;
   }
   __syncthreads();
