@@ -14,6 +14,7 @@ shape, timed with HIP events on its own stream) and the CPU baseline (the oracle
 restatement of the same step on this host's cores).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
+    python bench.py --pmc-driver      # only attention launches + a calibration copy, for rocprofv3 --pmc
 """
 
 from __future__ import annotations
@@ -114,6 +115,34 @@ def time_attention(config, cache, loop, iters: int = 50) -> dict:
     return {"us": us, "bytes": kv + qo}
 
 
+COPY_BYTES = 256 << 20  # calibration copy for the FETCH_SIZE / WRITE_SIZE counters
+TRAFFIC_FILE = ROOT / "profiles" / "paged_extend_traffic.md"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary (FETCH_SIZE +
+    WRITE_SIZE of both kernels, each scaled by the counter's reading for a copy of known size)."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
+def pmc_driver(config, cache, loop) -> None:
+    """Ten attention launches at the step's shape, then five device copies of COPY_BYTES: the
+    workload of the committed FETCH_SIZE / WRITE_SIZE runs."""
+    time_attention(config, cache, loop, iters=10)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("pmc driver done")
+
+
 def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict:
     """The oracle's torch-CPU restatement of one verify step (oracle/decoder.py) on this host."""
     from oracle import decoder as oracle_decoder  # the CPU baseline leg only
@@ -171,7 +200,8 @@ def main() -> int:
     p.add_argument("--max-n", type=int, default=4)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-steps", type=int, default=5)
+    p.add_argument("--cpu-steps", type=int, default=12)
+    p.add_argument("--pmc-driver", action="store_true", help="only attention launches + a calibration copy")
     p.add_argument("--cpu-warmup", type=int, default=1)
     args = p.parse_args()
 
@@ -191,6 +221,9 @@ def main() -> int:
                                    history_capacity=args.history + (args.k + 1) * (args.steps + args.warmup + 8),
                                    table_width=width, device=device)
     loop.load(histories, seq_lens, table)
+    if args.pmc_driver:
+        pmc_driver(config, cache, loop)
+        return 0
     log("capturing graph")
     loop.capture()
     for _ in range(args.warmup):
@@ -252,9 +285,10 @@ def main() -> int:
         "accepted_drafts_per_step": accepted_drafts / args.steps,
         "step_roofline": {"bound": "hbm", "bytes": traffic["total"], "achieved": step_gbs, "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
-        "roofline": {"kernel": "paged_extend_partial_kernel (paged verify attention, one layer)", "bound": "hbm",
-                     "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": attn_gbs / HBM_PEAK_GBS,
-                     "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"], "traffic": None},
+        "roofline": {"kernel": "paged verify attention, one layer (paged_extend_kernel + paged_extend_merge_kernel)",
+                     "bound": "hbm", "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": attn_gbs / HBM_PEAK_GBS, "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"],
+                     "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "wall_s_timed": wall,
     }

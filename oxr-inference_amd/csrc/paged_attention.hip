@@ -52,20 +52,19 @@ struct PairRegs {
 };
 
 __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict__ k_cache,
-                                          const bf16_t* __restrict__ v_cache, const int32_t* __restrict__ table_row,
-                                          int t0, int L, int kvh, int KV, int log2_bs, int64_t num_blocks, int r,
-                                          int g) {
+                                          const bf16_t* __restrict__ v_cache, const int* s_pages, int page0, int t0,
+                                          int L, int kvh, int KV, int log2_bs, int r, int g) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     // A 16-key tile lies inside one page (block_size >= 16, tiles aligned to
-    // 16), so its page number is wave-uniform: one scalar load, whose wait
-    // (lgkmcnt) does not hold back the vector loads already in flight.  Keys
-    // past L re-read key L - 1: their probabilities are exactly 0 and the
-    // cache rows below L hold finite values, so they add nothing.
+    // 16), so its page number is wave-uniform; it comes from the workgroup's
+    // copy of its page-table range in LDS, so no global table lookup sits
+    // between a step and the loads it prefetches.  Keys past L re-read key
+    // L - 1: their probabilities are exactly 0 and the cache rows below L
+    // hold finite values, so they add nothing.
     const int tile = __builtin_amdgcn_readfirstlane(min(t0 + 16 * p, L - 1));
-    int64_t blk = table_row[tile >> log2_bs];
-    blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);  // never leave the pool
-    const int64_t page = (blk << log2_bs) * KV * kD;                   // wave-uniform
+    const int64_t blk = __builtin_amdgcn_readfirstlane(s_pages[(tile >> log2_bs) - page0]);
+    const int64_t page = (blk << log2_bs) * KV * kD;  // wave-uniform
     const uint32_t tok = (uint32_t)min(t0 + 16 * p + r, L - 1);
     const uint32_t off = ((tok & ((1u << log2_bs) - 1)) * (uint32_t)KV + (uint32_t)kvh) * kD;
     const bf16_t* ks = k_cache + page + off + 32 * g;
@@ -87,7 +86,8 @@ __device__ __forceinline__ u32x4 selector(int r, int g, int shift) {
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-constexpr int kWaves = 8;  // waves per workgroup
+constexpr int kWaves = 8;          // waves per workgroup
+constexpr int kMaxSpanPages = 4096;  // page-table entries of one split, staged in LDS
 
 __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
@@ -96,6 +96,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     float* __restrict__ part_o, float* __restrict__ part_ml, bf16_t* __restrict__ out) {
   __shared__ float s_o[kWaves][kRows][kD];
   __shared__ float s_m[kWaves][kRows], s_l[kWaves][kRows];
+  __shared__ int s_pages[kMaxSpanPages];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int L = min(seq_lens[b], max_seq_len);  // max_seq_len <= table span, checked on the host
@@ -109,6 +110,13 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int r = lane & 15, g = lane >> 4;
   const int32_t* table_row = block_table + (int64_t)b * table_stride;
+  // This split's page numbers (clamped into the pool) into LDS.
+  const int page0 = t_begin >> log2_bs;
+  const int npages = t_end > t_begin ? ((t_end - 1) >> log2_bs) - page0 + 1 : 0;  // <= kMaxSpanPages (host check)
+  for (int i = tid; i < npages; i += 64 * kWaves) {
+    const int64_t blk = table_row[page0 + i];
+    s_pages[i] = (int)(blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk));  // never leave the pool
+  }
 
   // Q^T fragments for row r: q[b, s, kvh * G + hh, 32g + 8i .. +7].
   u32x4 qf[4];
@@ -124,6 +132,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     for (int i = 0; i < 4; ++i) qf[i] = u32x4{0u, 0u, 0u, 0u};
   }
   const u32x4 sel_lo = selector(r, g, 0), sel_hi = selector(r, g, 16);
+  __syncthreads();  // s_pages
 
   // Running row maximum of the raw scores (m_run) and the same in the exp2
   // domain (mc_run = m_run * scale * log2 e; 0 while every key is masked).
@@ -204,14 +213,13 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   if (n > 0) {
     const int t_last = t_first + (n - 1) * stride;
     PairRegs ra, rb;
-    load_pair(ra, k_cache, v_cache, table_row, t_first, L, kvh, KV, log2_bs, num_blocks, r, g);
+    load_pair(ra, k_cache, v_cache, s_pages, page0, t_first, L, kvh, KV, log2_bs, r, g);
     for (int i = 0; i < n; i += 2) {
       const int ta = t_first + i * stride;
-      load_pair(rb, k_cache, v_cache, table_row, min(ta + stride, t_last), L, kvh, KV, log2_bs, num_blocks, r, g);
+      load_pair(rb, k_cache, v_cache, s_pages, page0, min(ta + stride, t_last), L, kvh, KV, log2_bs, r, g);
       __builtin_amdgcn_sched_barrier(0);
       step(ra, ta);
-      load_pair(ra, k_cache, v_cache, table_row, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, num_blocks, r,
-                g);
+      load_pair(ra, k_cache, v_cache, s_pages, page0, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, r, g);
       __builtin_amdgcn_sched_barrier(0);
       if (i + 1 < n) step(rb, ta + stride);
     }
@@ -330,6 +338,11 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
   OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535, OXR_ERR_UNSUPPORTED);
   const int splits = splits_for(batch, num_kv_heads);
+  {
+    // One split's page-table range must fit the kernel's LDS copy.
+    const int64_t span_max = ((max_seq_len + splits - 1) / splits + 31) / 32 * 32;
+    OXR_RETURN_IF((span_max + block_size - 1) / block_size + 1 > kMaxSpanPages, OXR_ERR_UNSUPPORTED);
+  }
   int log2_bs = 0;
   while ((1 << log2_bs) < block_size) ++log2_bs;
   float* part_o = static_cast<float*>(workspace);
