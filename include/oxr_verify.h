@@ -182,6 +182,29 @@ int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16*
                      size_t workspace_bytes, oxr_stream_t stream);
 
 /*
+ * (3b) (2b) followed by (3) in one launch: the attention block of the decoder
+ * layer's extend (oxr_runtime/language.py:311-316: kernels.qk_norm_rope_store
+ * from _attention_inputs, language.py:260-263, then attention.paged_extend)
+ * without the q round trip through memory.  Takes the qkv
+ * projection bf16 [B * S, H + 2 KV, 128] of the S new tokens of each sequence
+ * (token b * S + s) with the arguments of (2b) (no k_out / v_out) and of (3)
+ * (no q).  Each new token's K (normed, rotated) and V are stored at its slot
+ * exactly as (2b) stores them, by the workgroup whose keys contain its position
+ * seq_lens[b] - S + s, before that workgroup reads them; slots must hold the
+ * cache locations of those positions under block_table (as the verify step
+ * assembles them).  Same requirements and workspace as (3); bit-identical q,
+ * cache rows and output to (2b) then (3).
+ */
+int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                                  const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,
+                                  const int64_t* positions, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache,
+                                  const int64_t* slots, int64_t num_slots, const int32_t* seq_lens,
+                                  const int32_t* block_table, int64_t table_stride, int32_t batch,
+                                  int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale,
+                                  oxr_bf16* out, void* workspace, size_t workspace_bytes, oxr_stream_t stream);
+
+/*
  * (4a) Weight-streaming bf16 GEMM Y = X * W^T with a fused epilogue.
  * Replaces the nn.Linear projections of the verify forward (language.py:261
  * qkv_proj, 268 o_proj, 269 gate_up_proj/down_proj) together with the

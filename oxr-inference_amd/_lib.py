@@ -37,6 +37,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I32, _F32, _P, _P, _SZ, _P],
     ),
+    "oxr_qk_norm_rope_paged_extend": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _I64, _P, _F32, _P, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32,
+         _I64, _I32, _F32, _P, _P, _SZ, _P],
+    ),
     "oxr_qk_norm_rope_store_at": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _F32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _P],

@@ -58,3 +58,51 @@ def paged_extend(
         _lib.stream(device),
     )
     return out
+
+
+def qk_norm_rope_paged_extend(
+    qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, cos_table: torch.Tensor,
+    sin_table: torch.Tensor, positions: torch.Tensor, eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
+    slots: torch.Tensor, seq_lens: torch.Tensor, block_table: torch.Tensor, num_heads: int, *,
+    scale: float | None = None, max_seq_len: int | None = None, out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The decoder layer's attention block of the verify step (oxr_runtime/language.py:311-316) in one
+    launch: ``kernels.qk_norm_rope_store`` (q/k RMSNorm + RoPE at ``positions``, K/V into the cache at
+    ``slots``) followed by :func:`paged_extend`, with q kept on chip.  ``qkv`` is ``[B*S, (H+2KV)*D]``
+    for the S new tokens of each of the B sequences; returns ``[B, S, H, D]`` and leaves the cache
+    rows exactly as the two separate calls would."""
+    device = _lib.require_gpu(qkv, q_weight, k_weight, cos_table, sin_table, positions, k_cache, v_cache, slots,
+                              seq_lens, block_table, name="qk_norm_rope_paged_extend")
+    _lib.require(qkv.dtype == torch.bfloat16 and qkv.dim() == 2 and qkv.is_contiguous(), "qkv must be contiguous bf16")
+    _lib.require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "caches must be [blocks, block_size, KV, D]")
+    _lib.require(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    num_blocks, block_size, kv, d = k_cache.shape
+    b = seq_lens.shape[0]
+    n = qkv.shape[0]
+    _lib.require(b > 0 and n % b == 0 and qkv.shape[1] == (num_heads + 2 * kv) * d, "qkv shape mismatch")
+    s = n // b
+    _lib.require(positions.dtype == torch.int64 and positions.shape == (n,), "positions must be int64 [B*S]")
+    _lib.require(slots.dtype == torch.int64 and slots.shape == (n,), "slots must be int64 [B*S]")
+    _lib.require(seq_lens.dtype == torch.int32 and block_table.dtype == torch.int32 and block_table.stride(1) == 1,
+                 "seq_lens / block_table must be int32, table rows contiguous")
+    _lib.require(cos_table.dim() == 2 and cos_table.shape == sin_table.shape and cos_table.shape[1] == d // 2,
+                 "cos/sin tables must be [rows, D/2]")
+    if max_seq_len is None:
+        max_seq_len = block_table.shape[1] * block_size
+    if scale is None:
+        scale = d ** -0.5
+    if out is None:
+        out = torch.empty(b, s, num_heads, d, dtype=torch.bfloat16, device=device)
+    need = workspace_bytes(b, kv, max_seq_len)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    _lib.call(
+        "oxr_qk_norm_rope_paged_extend", qkv.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(),
+        cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0], positions.data_ptr(), float(eps),
+        k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), num_blocks * block_size, seq_lens.data_ptr(),
+        block_table.data_ptr(), block_table.stride(0), b, s, num_heads, kv, d, block_size, num_blocks, max_seq_len,
+        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _lib.stream(device),
+    )
+    return out

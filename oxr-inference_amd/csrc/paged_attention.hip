@@ -35,7 +35,7 @@
 //     standing for key 16p + 4g + j; accumulators hold O^T[d][r], so the
 //     per-row rescale is a per-lane scalar.
 // The next 32 keys' K and V are loaded before the current ones are used.
-#include "common.h"
+#include "norm_rope.h"
 
 namespace oxr {
 namespace {
@@ -89,12 +89,35 @@ __device__ __forceinline__ u32x4 selector(int r, int g, int shift) {
 constexpr int kWaves = 8;          // waves per workgroup
 constexpr int kMaxSpanPages = 4096;  // page-table entries of one split, staged in LDS
 
+// Inputs of the fused q/k norm + RoPE + KV store (oxr_qk_norm_rope_paged_extend).
+struct RopeArgs {
+  const bf16_t* qkv;  // [B * S, H + 2 KV, 128]: the qkv projection of the new tokens
+  const bf16_t* q_weight;
+  const bf16_t* k_weight;
+  const bf16_t* cos_table;  // [table_rows, 64]
+  const bf16_t* sin_table;
+  int64_t table_rows;
+  const int64_t* positions;  // [B * S] RoPE table row of each token
+  const int64_t* slots;      // [B * S] cache slot of each token (outside [0, num_slots): not stored)
+  int64_t num_slots;
+  float eps;
+  bf16_t* k_store;  // the caches the kernel reads, for the new rows
+  bf16_t* v_store;
+};
+
+// kFused: q comes from qkv through norm + RoPE (done here, into LDS), and the
+// new tokens' K (norm + RoPE) and V rows are written to the cache by the
+// workgroup whose key range holds their positions, before any wave reads them;
+// otherwise q is read as given.  The caches are plain (not restrict) pointers
+// because the fused kernel writes the rows it later reads.
+template <bool kFused>
 __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ block_table, int64_t table_stride, int S,
-    int H, int KV, int log2_bs, int64_t num_blocks, float scale_log2, int max_seq_len, int splits,
-    float* __restrict__ part_o, float* __restrict__ part_ml, bf16_t* __restrict__ out) {
+    const bf16_t* __restrict__ q, const bf16_t* k_cache, const bf16_t* v_cache, const int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ block_table, int64_t table_stride, int S, int H, int KV, int log2_bs,
+    int64_t num_blocks, float scale_log2, int max_seq_len, int splits, float* __restrict__ part_o,
+    float* __restrict__ part_ml, bf16_t* __restrict__ out, RopeArgs ra) {
   __shared__ float s_o[kWaves][kRows][kD];
+  __shared__ u32x4 s_q[kFused ? kRows : 1][kD / 8];
   __shared__ float s_m[kWaves][kRows], s_l[kWaves][kRows];
   __shared__ int s_pages[kMaxSpanPages];
 
@@ -118,21 +141,67 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     s_pages[i] = (int)(blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk));  // never leave the pool
   }
 
+  if constexpr (kFused) {
+    // 32 jobs of one 128-element row on 16 lanes: q rows [0, R), then the K
+    // rows and the V rows of the S new tokens.  Lanes without a job redo row
+    // 0 (every lane must take part in the exchanges) and store nothing.
+    const int job = tid >> 4, s16 = tid & 15;
+    const int jk = R, jv = R + S, jend = R + 2 * S;
+    const int jj = job < jend ? job : 0;
+    int ss, head;
+    if (jj < jk) {
+      ss = jj / G;
+      head = kvh * G + jj % G;
+    } else if (jj < jv) {
+      ss = jj - jk;
+      head = H + kvh;
+    } else {
+      ss = jj - jv;
+      head = H + KV + kvh;
+    }
+    const int64_t tok = (int64_t)b * S + ss;
+    const u32x4 raw = ld128(ra.qkv + (tok * (H + 2 * KV) + head) * kD + s16 * 8);
+    int64_t trow = ra.positions[tok];
+    trow = trow < 0 ? 0 : (trow >= ra.table_rows ? ra.table_rows - 1 : trow);
+    const u32x4 normed = norm_rope_16(raw, jj < jk ? ra.q_weight : ra.k_weight, ra.cos_table + trow * (kD / 2),
+                                      ra.sin_table + trow * (kD / 2), ra.eps, s16);
+    if (job < jk) {
+      s_q[jj][s16] = normed;
+    } else if (job < jend) {
+      // Written by the workgroup whose keys hold the token's position, so
+      // each new row is stored once and read only by this workgroup.
+      const int pos = L - S + ss;
+      const int64_t slot = ra.slots[tok];
+      if (pos >= t_begin && pos < t_end && slot >= 0 && slot < ra.num_slots) {
+        bf16_t* dst = (job < jv ? ra.k_store : ra.v_store) + (slot * KV + kvh) * kD + s16 * 8;
+        st128(dst, job < jv ? normed : raw);
+      }
+    }
+  }
+
   // Q^T fragments for row r: q[b, s, kvh * G + hh, 32g + 8i .. +7].
   u32x4 qf[4];
   int qpos = -1;  // absolute position of row r; keys after it are masked
   if (r < R) {
     const int s = r / G, hh = r % G;
-    const bf16_t* src = q + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + 32 * g;
+    if constexpr (!kFused) {
+      const bf16_t* src = q + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + 32 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qf[i] = ld128(src + 8 * i);
+      for (int i = 0; i < 4; ++i) qf[i] = ld128(src + 8 * i);
+    }
     qpos = L - S + s;
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) qf[i] = u32x4{0u, 0u, 0u, 0u};
   }
   const u32x4 sel_lo = selector(r, g, 0), sel_hi = selector(r, g, 16);
-  __syncthreads();  // s_pages
+  __syncthreads();  // s_pages; fused: s_q and the new K/V rows
+  if constexpr (kFused) {
+    if (r < R) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qf[i] = s_q[r][4 * g + i];
+    }
+  }
 
   // Running row maximum of the raw scores (m_run) and the same in the exp2
   // domain (mc_run = m_run * scale * log2 e; 0 while every key is masked).
@@ -317,13 +386,16 @@ extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv
   return units * kRows * (kD + 2) * sizeof(float);
 }
 
-extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache,
-                                const int32_t* seq_lens, const int32_t* block_table, int64_t table_stride,
-                                int32_t batch, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
-                                int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_seq_len,
-                                float scale, oxr_bf16* out, void* workspace, size_t workspace_bytes,
-                                oxr_stream_t stream) {
-  using namespace oxr;
+namespace oxr {
+namespace {
+
+// Checks, split count and the two launches shared by both entry points; `ra`
+// is null for the unfused one.
+int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache, const int32_t* seq_lens,
+                        const int32_t* block_table, int64_t table_stride, int32_t batch, int32_t tokens_per_seq,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out, void* workspace,
+                        size_t workspace_bytes, const RopeArgs* ra, hipStream_t s) {
   OXR_RETURN_IF(batch < 0 || tokens_per_seq <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
                     table_stride < 0 || max_seq_len <= 0,
                 OXR_ERR_INVALID_ARG);
@@ -333,7 +405,7 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
   // Contexts are clamped to max_seq_len, so every key visited maps to a table entry.
   OXR_RETURN_IF((int64_t)max_seq_len > table_stride * block_size, OXR_ERR_INVALID_ARG);
   if (batch == 0) return OXR_OK;
-  OXR_RETURN_IF(!q || !k_cache || !v_cache || !seq_lens || !block_table || !out, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF((!ra && !q) || !k_cache || !v_cache || !seq_lens || !block_table || !out, OXR_ERR_INVALID_ARG);
   const size_t need = oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
   OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535, OXR_ERR_UNSUPPORTED);
@@ -348,13 +420,55 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)batch * num_kv_heads * splits * kRows * kD;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(paged_extend_kernel, dim3(splits, num_kv_heads, batch), dim3(64 * kWaves), 0, s, q, k_cache,
-                     v_cache, seq_lens, block_table, table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs,
-                     num_blocks, scale_log2, max_seq_len, splits, part_o, part_ml, out);
+  const dim3 grid(splits, num_kv_heads, batch), block(64 * kWaves);
+  if (ra) {
+    hipLaunchKernelGGL(paged_extend_kernel<true>, grid, block, 0, s, nullptr, k_cache, v_cache, seq_lens, block_table,
+                       table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
+                       max_seq_len, splits, part_o, part_ml, out, *ra);
+  } else {
+    hipLaunchKernelGGL(paged_extend_kernel<false>, grid, block, 0, s, q, k_cache, v_cache, seq_lens, block_table,
+                       table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
+                       max_seq_len, splits, part_o, part_ml, out, RopeArgs{});
+  }
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;
   hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(256), 0, s, part_o, part_ml,
                      seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, out);
   return OXR_LAUNCH_STATUS();
+}
+
+}  // namespace
+}  // namespace oxr
+
+extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache,
+                                const int32_t* seq_lens, const int32_t* block_table, int64_t table_stride,
+                                int32_t batch, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_seq_len,
+                                float scale, oxr_bf16* out, void* workspace, size_t workspace_bytes,
+                                oxr_stream_t stream) {
+  return oxr::launch_paged_extend(q, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
+                                  num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
+                                  workspace, workspace_bytes, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                                             const oxr_bf16* cos_table, const oxr_bf16* sin_table,
+                                             int64_t table_rows, const int64_t* positions, float eps,
+                                             oxr_bf16* k_cache, oxr_bf16* v_cache, const int64_t* slots,
+                                             int64_t num_slots, const int32_t* seq_lens, const int32_t* block_table,
+                                             int64_t table_stride, int32_t batch, int32_t tokens_per_seq,
+                                             int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale,
+                                             oxr_bf16* out, void* workspace, size_t workspace_bytes,
+                                             oxr_stream_t stream) {
+  using namespace oxr;
+  OXR_RETURN_IF(num_slots < 0, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(batch > 0 && (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || table_rows <= 0 ||
+                              !positions || !slots),
+                OXR_ERR_INVALID_ARG);
+  const RopeArgs ra{qkv, q_weight, k_weight, cos_table, sin_table, table_rows, positions, slots, num_slots, eps,
+                    k_cache, v_cache};
+  return launch_paged_extend(nullptr, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
+                             num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
+                             workspace, workspace_bytes, &ra, (hipStream_t)stream);
 }

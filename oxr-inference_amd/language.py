@@ -5,8 +5,8 @@ Per layer (language.py:301-317 with the fused projections of :234-245):
 
     h        = rms_norm(residual)                               oxr_rms_norm / oxr_embed_rms_norm
     qkv      = h @ Wqkv^T                                       oxr_gemm_bf16
-    q        = qk_norm_rope_store(qkv, ...)  (K/V -> cache)     oxr_qk_norm_rope_store_at
-    attn     = paged_extend(q, cache, seq_lens, block_table)    oxr_paged_extend
+    q        = qk_norm_rope_store(qkv, ...)  (K/V -> cache)     } one launch:
+    attn     = paged_extend(q, cache, seq_lens, block_table)    } oxr_qk_norm_rope_paged_extend
     o_part   = k-split fp32 sums of attn @ Wo^T                 oxr_gemm_bf16_partial
     residual = bf16(bf16(sum o_part) + residual); h = rms_norm  oxr_add_partials_rms_norm
     act      = silu(h @ Wg^T) * (h @ Wu^T)                      oxr_gemm_bf16 (SiLU*mul epilogue)
@@ -139,7 +139,6 @@ class StepBuffers:
     residual: torch.Tensor
     h: torch.Tensor
     qkv: torch.Tensor
-    q: torch.Tensor
     attn: torch.Tensor
     act: torch.Tensor
     attn_workspace: torch.Tensor
@@ -159,7 +158,6 @@ class StepBuffers:
         return cls(
             residual=torch.zeros(t, config.hidden_size, **bf), h=torch.zeros(t, config.hidden_size, **bf),
             qkv=torch.zeros(t, config.qkv_size, **bf),
-            q=torch.zeros(max_batch, tokens_per_seq, config.num_heads, config.head_dim, **bf),
             attn=torch.zeros(max_batch, tokens_per_seq, config.num_heads, config.head_dim, **bf),
             act=torch.zeros(t, config.intermediate_size, **bf),
             attn_workspace=torch.zeros(max(attention.workspace_bytes(max_batch, config.num_kv_heads, max_seq_len), 1),
@@ -236,12 +234,10 @@ class LanguageModel:
         b, s = batch.block_table.shape[0], batch.tokens_per_seq
         t = b * s
         stream = _lib.stream(batch.positions.device)
-        res, h = buffers.residual[:t], buffers.h[:t]
-        qkv, q = buffers.qkv[:t], buffers.q[:b]
+        h = buffers.h[:t]
+        qkv = buffers.qkv[:t]
         attn, act = buffers.attn[:b], buffers.act[:t]
-        q_flat = q.view(t, c.num_heads, c.head_dim)
         attn_flat = attn.view(t, c.num_heads * c.head_dim)
-        num_slots = cache.num_blocks * cache.block_size
         max_seq_len = min(buffers.max_seq_len, batch.block_table.shape[1] * cache.block_size)
         eps = float(c.rms_norm_eps)
         for index in range(start, stop):
@@ -250,14 +246,11 @@ class LanguageModel:
                 self._settle_norm(buffers, t, layer.input_norm, stream)
             gemm.linear(h, layer.qkv, out=qkv)
             k_cache, v_cache = cache.k[index], cache.v[index]
-            _lib.call(
-                "oxr_qk_norm_rope_store_at", qkv.data_ptr(), layer.q_norm.data_ptr(), layer.k_norm.data_ptr(),
-                w.rope_cos.data_ptr(), w.rope_sin.data_ptr(), w.rope_cos.shape[0], batch.positions.data_ptr(), eps,
-                k_cache.data_ptr(), v_cache.data_ptr(), batch.slots.data_ptr(), num_slots, t, c.num_heads,
-                c.num_kv_heads, c.head_dim, q_flat.data_ptr(), None, None, stream,
+            attention.qk_norm_rope_paged_extend(
+                qkv, layer.q_norm, layer.k_norm, w.rope_cos, w.rope_sin, batch.positions, eps, k_cache, v_cache,
+                batch.slots, batch.seq_lens, batch.block_table, c.num_heads, scale=c.head_dim ** -0.5,
+                max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace,
             )
-            attention.paged_extend(q, k_cache, v_cache, batch.seq_lens, batch.block_table, scale=c.head_dim ** -0.5,
-                                   max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace)
             buffers.pending_splits = gemm.linear_partial(attn_flat, layer.o, buffers.partials)
             self._settle_norm(buffers, t, layer.post_norm, stream)
             gemm.linear_silu_mul(h, layer.gate_up, out=act)

@@ -1,0 +1,91 @@
+"""The fused attention block (q/k norm + RoPE + K/V store + paged attention in one launch) against
+the two separate calls it replaces: the output and every cache row must be bit-identical.
+
+Contexts are chosen so the S new tokens fall inside one context split, straddle two splits, or
+fill a split of their own; S=1, S=4 and S=8 (16 query rows per kv head) and block sizes 16 and
+256 are covered, as is a slot outside the cache (skipped by both paths).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, pkg
+
+pytestmark = pytest.mark.gpu
+attention = pkg("attention")
+_lib = pkg("_lib")
+
+
+def _case(seq_lens, S, H, KV, block_size, seed, bad_slot=False):
+    rng = np.random.default_rng(seed)
+    B = len(seq_lens)
+    seq_lens = np.asarray(seq_lens, dtype=np.int32)
+    need = (seq_lens + block_size - 1) // block_size
+    width = int(need.max()) + 1
+    num_blocks = int(need.sum()) + 8
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    table = np.zeros((B, width), dtype=np.int32)
+    off = 0
+    for b in range(B):
+        table[b, : need[b]] = perm[off : off + need[b]]
+        off += need[b]
+    positions = np.concatenate([np.arange(L - S, L) for L in seq_lens]).astype(np.int64)
+    slots = np.array([table[i // S, p // block_size] * block_size + p % block_size for i, p in enumerate(positions)],
+                     dtype=np.int64)
+    if bad_slot:
+        slots[1] = num_blocks * block_size + 5  # outside the cache: neither path stores it
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = "cuda"
+    kc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device=dev).to(torch.bfloat16)
+    qkv = torch.randn(B * S, (H + 2 * KV) * 128, generator=g, device=dev).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    rows = int(seq_lens.max()) + 4
+    ang = torch.rand(rows, 64, generator=g, device=dev) * 6.283
+    cos, sin = torch.cos(ang).to(torch.bfloat16), torch.sin(ang).to(torch.bfloat16)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    seq_t, table_t, pos_t, slots_t = t(seq_lens), t(table), t(positions), t(slots)
+    eps = 1e-6
+
+    # Separate: oxr_qk_norm_rope_store_at, then oxr_paged_extend.
+    k1, v1 = kc.clone(), vc.clone()
+    q = torch.empty(B, S, H, 128, dtype=torch.bfloat16, device=dev)
+    _lib.call("oxr_qk_norm_rope_store_at", qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(),
+              sin.data_ptr(), rows, pos_t.data_ptr(), eps, k1.data_ptr(), v1.data_ptr(), slots_t.data_ptr(),
+              num_blocks * block_size, B * S, H, KV, 128, q.data_ptr(), None, None, _lib.stream(torch.device(dev)))
+    out1 = attention.paged_extend(q, k1, v1, seq_t, table_t)
+
+    # Fused.
+    k2, v2 = kc.clone(), vc.clone()
+    out2 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k2, v2, slots_t, seq_t, table_t, H)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), "attention output differs"
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16)), "K cache differs"
+    assert torch.equal(v1.view(torch.int16), v2.view(torch.int16)), "V cache differs"
+
+
+@pytest.mark.parametrize("S", [1, 4, 8])
+def test_small_contexts_straddling_splits(S) -> None:
+    lens = [33, 64, 65, 66, 67, 95, 96, 97]
+    announce(f"fused attention S={S} lens={lens}")
+    _case(lens, S, 16, 8, 16, seed=S)
+
+
+def test_verify_step_shape_and_ragged() -> None:
+    lens = [4100, 4096 + 5, 2051, 8192, 300, 4127, 4128, 4129]
+    announce(f"fused attention verify shape lens={lens}")
+    _case(lens, 4, 16, 8, 16, seed=11)
+
+
+def test_block_256_and_skipped_slot() -> None:
+    announce("fused attention block 256, one slot outside the cache")
+    _case([700, 257, 1300, 90], 4, 16, 8, 256, seed=12, bad_slot=True)
+
+
+def test_single_sequence_many_splits() -> None:
+    announce("fused attention B=1 (32 splits)")
+    _case([5000], 4, 16, 8, 16, seed=13)
