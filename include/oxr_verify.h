@@ -192,8 +192,11 @@ int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16*
  * exactly as (2b) stores them, by the workgroup whose keys contain its position
  * seq_lens[b] - S + s, before that workgroup reads them; slots must hold the
  * cache locations of those positions under block_table (as the verify step
- * assembles them).  Same requirements and workspace as (3); bit-identical q,
- * cache rows and output to (2b) then (3).
+ * assembles them).  A slot outside [0, num_slots) is not stored, as in
+ * (2b), but the token's computed K/V still take part in the attention.
+ * Same requirements and workspace as (3), and also
+ * tokens_per_seq <= 8 with tokens_per_seq * (H / KV + 2) <= 32; bit-identical
+ * q, cache rows and output to (2b) then (3).
  */
 int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
                                   const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,

@@ -41,12 +41,11 @@ __device__ __forceinline__ u32x4 pack8(const float (&v)[8]) {
   return w;
 }
 
-// raw: this lane's 8 elements of the head row; weight: the norm weight (128);
-// cos_row / sin_row: the RoPE table row of the token's position (64 each).
-// Returns the lane's 8 output elements, packed bf16.
-__device__ __forceinline__ u32x4 norm_rope_16(const u32x4& raw, const bf16_t* __restrict__ weight,
-                                              const bf16_t* __restrict__ cos_row,
-                                              const bf16_t* __restrict__ sin_row, float eps, int s) {
+// raw: this lane's 8 elements of the head row; w8: its 8 norm weights
+// (weight[8s .. 8s+7]); c8 / s8: cos / sin[8 (s % 8) .. +7] of the RoPE table
+// row of the token's position.  Returns the lane's 8 outputs, packed bf16.
+__device__ __forceinline__ u32x4 norm_rope_16v(const u32x4& raw, const u32x4& w8, const u32x4& c8, const u32x4& s8,
+                                               float eps, int s) {
   float x[8];
   unpack8(raw, x);
   float q2[8];
@@ -65,22 +64,30 @@ __device__ __forceinline__ u32x4 norm_rope_16(const u32x4& raw, const bf16_t* __
   const float r = 1.0f / sqrtf(var + eps);
 
   float w[8], y[8];
-  unpack8(ld128(weight + s * 8), w);
+  unpack8(w8, w);
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = round_bf16(w[e] * round_bf16(x[e] * r));
 
   // NeoX rotation: element j of the first half pairs with j of the second,
   // which lives in lane s ^ 8 at the same register position.
   float c[8], sn[8], out[8];
-  const int j0 = (s & 7) * 8;
-  unpack8(ld128(cos_row + j0), c);
-  unpack8(ld128(sin_row + j0), sn);
+  unpack8(c8, c);
+  unpack8(s8, sn);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float other = shfl_xor_f(y[e], 8);
     out[e] = (s < 8) ? (y[e] * c[e] - other * sn[e]) : (other * sn[e] + y[e] * c[e]);
   }
   return pack8(out);
+}
+
+// The same with the weights and the table row read here (weight: [128];
+// cos_row / sin_row: [64]).
+__device__ __forceinline__ u32x4 norm_rope_16(const u32x4& raw, const bf16_t* __restrict__ weight,
+                                              const bf16_t* __restrict__ cos_row,
+                                              const bf16_t* __restrict__ sin_row, float eps, int s) {
+  const int j0 = (s & 7) * 8;
+  return norm_rope_16v(raw, ld128(weight + s * 8), ld128(cos_row + j0), ld128(sin_row + j0), eps, s);
 }
 
 }  // namespace oxr

@@ -88,6 +88,7 @@ __device__ __forceinline__ u32x4 selector(int r, int g, int shift) {
 
 constexpr int kWaves = 8;          // waves per workgroup
 constexpr int kMaxSpanPages = 4096;  // page-table entries of one split, staged in LDS
+constexpr int kMaxNew = 8;           // new tokens per sequence (S) of the fused kernel
 
 // Inputs of the fused q/k norm + RoPE + KV store (oxr_qk_norm_rope_paged_extend).
 struct RopeArgs {
@@ -118,10 +119,48 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     float* __restrict__ part_ml, bf16_t* __restrict__ out, RopeArgs ra) {
   __shared__ float s_o[kWaves][kRows][kD];
   __shared__ u32x4 s_q[kFused ? kRows : 1][kD / 8];
+  __shared__ u32x4 s_newk[kFused ? kMaxNew : 1][kD / 8], s_newv[kFused ? kMaxNew : 1][kD / 8];
   __shared__ float s_m[kWaves][kRows], s_l[kWaves][kRows];
   __shared__ int s_pages[kMaxSpanPages];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = H / KV, R = S * G;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int r = lane & 15, g = lane >> 4;
+
+  // Fused: 32 jobs of one 128-element row on 16 lanes -- q rows [0, R), then
+  // the K rows and the V rows of the S new tokens.  Lanes without a job redo
+  // row 0 (every lane must take part in the norm's exchanges) and store
+  // nothing.  Their loads go out first: none depends on the context length.
+  int f_job = 0, f_s16 = 0, f_jk = 0, f_jv = 0, f_jend = 0, f_jj = 0, f_ss = 0;
+  int64_t f_trow = 0, f_slot = -1;
+  u32x4 f_raw = {0u, 0u, 0u, 0u}, f_w8 = {0u, 0u, 0u, 0u};
+  if constexpr (kFused) {
+    f_job = tid >> 4;
+    f_s16 = tid & 15;
+    f_jk = R;
+    f_jv = R + S;
+    f_jend = R + 2 * S;
+    f_jj = f_job < f_jend ? f_job : 0;
+    int head;
+    if (f_jj < f_jk) {
+      f_ss = f_jj / G;
+      head = kvh * G + f_jj % G;
+    } else if (f_jj < f_jv) {
+      f_ss = f_jj - f_jk;
+      head = H + kvh;
+    } else {
+      f_ss = f_jj - f_jv;
+      head = H + KV + kvh;
+    }
+    const int64_t tok = (int64_t)b * S + f_ss;
+    f_raw = ld128(ra.qkv + (tok * (H + 2 * KV) + head) * kD + f_s16 * 8);
+    f_w8 = ld128((f_jj < f_jk ? ra.q_weight : ra.k_weight) + f_s16 * 8);
+    f_slot = ra.slots[tok];
+    f_trow = ra.positions[tok];
+    f_trow = f_trow < 0 ? 0 : (f_trow >= ra.table_rows ? ra.table_rows - 1 : f_trow);
+  }
+
   const int L = min(seq_lens[b], max_seq_len);  // max_seq_len <= table span, checked on the host
   // This workgroup's keys: split `split` of [0, L), in whole 32-key pairs.
   const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
@@ -129,9 +168,6 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   const int t_end = min(L, t_begin + span);
   const bool single = L <= span;  // the whole context is in split 0
   if (single && split > 0) return;
-  const int G = H / KV, R = S * G;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int r = lane & 15, g = lane >> 4;
   const int32_t* table_row = block_table + (int64_t)b * table_stride;
   // This split's page numbers (clamped into the pool) into LDS.
   const int page0 = t_begin >> log2_bs;
@@ -142,44 +178,29 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   }
 
   if constexpr (kFused) {
-    // 32 jobs of one 128-element row on 16 lanes: q rows [0, R), then the K
-    // rows and the V rows of the S new tokens.  Lanes without a job redo row
-    // 0 (every lane must take part in the exchanges) and store nothing.
-    const int job = tid >> 4, s16 = tid & 15;
-    const int jk = R, jv = R + S, jend = R + 2 * S;
-    const int jj = job < jend ? job : 0;
-    int ss, head;
-    if (jj < jk) {
-      ss = jj / G;
-      head = kvh * G + jj % G;
-    } else if (jj < jv) {
-      ss = jj - jk;
-      head = H + kvh;
-    } else {
-      ss = jj - jv;
-      head = H + KV + kvh;
-    }
-    const int64_t tok = (int64_t)b * S + ss;
-    const u32x4 raw = ld128(ra.qkv + (tok * (H + 2 * KV) + head) * kD + s16 * 8);
-    int64_t trow = ra.positions[tok];
-    trow = trow < 0 ? 0 : (trow >= ra.table_rows ? ra.table_rows - 1 : trow);
-    const u32x4 normed = norm_rope_16(raw, jj < jk ? ra.q_weight : ra.k_weight, ra.cos_table + trow * (kD / 2),
-                                      ra.sin_table + trow * (kD / 2), ra.eps, s16);
-    if (job < jk) {
-      s_q[jj][s16] = normed;
-    } else if (job < jend) {
-      // Written by the workgroup whose keys hold the token's position, so
-      // each new row is stored once and read only by this workgroup.
-      const int pos = L - S + ss;
-      const int64_t slot = ra.slots[tok];
-      if (pos >= t_begin && pos < t_end && slot >= 0 && slot < ra.num_slots) {
-        bf16_t* dst = (job < jv ? ra.k_store : ra.v_store) + (slot * KV + kvh) * kD + s16 * 8;
-        st128(dst, job < jv ? normed : raw);
+    // The new tokens' rows, computed now that the table row of each position
+    // has arrived (its load was issued with the rows'); see the top of the
+    // kernel for the job layout.
+    const u32x4 c8 = ld128(ra.cos_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
+    const u32x4 sn8 = ld128(ra.sin_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
+    const u32x4 normed = norm_rope_16v(f_raw, f_w8, c8, sn8, ra.eps, f_s16);
+    if (f_job < f_jk) {
+      s_q[f_jj][f_s16] = normed;
+    } else if (f_job < f_jend) {
+      // Kept in LDS for this workgroup's own reads of the new rows, and
+      // written to the cache by the workgroup whose keys hold the token's
+      // position (each row stored once; nothing in this launch reads it back
+      // from memory, so the stores need not complete before the loop).
+      if (f_job < f_jv) s_newk[f_ss][f_s16] = normed;
+      else s_newv[f_ss][f_s16] = f_raw;
+      const int pos = L - S + f_ss;
+      if (pos >= t_begin && pos < t_end && f_slot >= 0 && f_slot < ra.num_slots) {
+        bf16_t* dst = (f_job < f_jv ? ra.k_store : ra.v_store) + (f_slot * KV + kvh) * kD + f_s16 * 8;
+        st128(dst, f_job < f_jv ? normed : f_raw);
       }
     }
   }
 
-  // Q^T fragments for row r: q[b, s, kvh * G + hh, 32g + 8i .. +7].
   u32x4 qf[4];
   int qpos = -1;  // absolute position of row r; keys after it are masked
   if (r < R) {
@@ -195,7 +216,11 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     for (int i = 0; i < 4; ++i) qf[i] = u32x4{0u, 0u, 0u, 0u};
   }
   const u32x4 sel_lo = selector(r, g, 0), sel_hi = selector(r, g, 16);
-  __syncthreads();  // s_pages; fused: s_q and the new K/V rows
+  // LDS (s_pages; fused: s_q and the new K/V rows) is complete; global loads
+  // and stores stay in flight across the barrier.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   if constexpr (kFused) {
     if (r < R) {
 #pragma unroll
@@ -213,7 +238,21 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   // The waves take pairs wave, wave + 8, ... so at any time the workgroup reads
   // 8 neighbouring pairs of the same pages.
   const int stride = 32 * kWaves;
-  auto step = [&](const PairRegs& cur, const int t0) {
+  auto step = [&](PairRegs& cur, const int t0) {
+    if constexpr (kFused) {
+      if (t0 + 31 >= L - S) {  // wave-uniform: the pair holds new tokens, whose rows come from LDS
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int ns = min(t0 + 16 * p + r, L - 1) - (L - S);  // keys past L re-read row L - 1
+          if (ns >= 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur.k[p][i] = s_newk[ns][4 * g + i];  // dims 32g + 8i
+#pragma unroll
+            for (int c = 0; c < 4; ++c) cur.v[p][c] = s_newv[ns][4 * c + g];  // dims 32c + 8g
+          }
+        }
+      }
+    }
     // Raw scores of keys t0 + 16p + 4g + j for query row r.
     float sv[8];
 #pragma unroll
@@ -463,6 +502,10 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
                                              oxr_stream_t stream) {
   using namespace oxr;
   OXR_RETURN_IF(num_slots < 0, OXR_ERR_INVALID_ARG);
+  // One 16-lane job per q row and per new K and V row: 32 per workgroup.
+  OXR_RETURN_IF(num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+                    (tokens_per_seq > kMaxNew || tokens_per_seq * (num_heads / num_kv_heads + 2) > 32),
+                OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(batch > 0 && (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || table_rows <= 0 ||
                               !positions || !slots),
                 OXR_ERR_INVALID_ARG);

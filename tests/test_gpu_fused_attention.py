@@ -3,7 +3,8 @@ the two separate calls it replaces: the output and every cache row must be bit-i
 
 Contexts are chosen so the S new tokens fall inside one context split, straddle two splits, or
 fill a split of their own; S=1, S=4 and S=8 (16 query rows per kv head) and block sizes 16 and
-256 are covered, as is a slot outside the cache (skipped by both paths).
+256 are covered, as is a slot outside the cache (not stored by either path; only the sequence
+that owns it may then differ, since the fused kernel attends to the token's computed row).
 """
 
 from __future__ import annotations
@@ -63,6 +64,11 @@ def _case(seq_lens, S, H, KV, block_size, seed, bad_slot=False):
     k2, v2 = kc.clone(), vc.clone()
     out2 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k2, v2, slots_t, seq_t, table_t, H)
     torch.cuda.synchronize()
+    if bad_slot:
+        # The row with no valid slot is not stored by either path; the fused kernel still attends to
+        # the token's computed row, the separate calls to whatever the cache held.  Sequence 0 owns
+        # that token; every other sequence must match exactly.
+        out1, out2 = out1[1:], out2[1:]
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), "attention output differs"
     assert torch.equal(k1.view(torch.int16), k2.view(torch.int16)), "K cache differs"
     assert torch.equal(v1.view(torch.int16), v2.view(torch.int16)), "V cache differs"
