@@ -51,20 +51,29 @@ struct PairRegs {
   u32x4 v[2][4];  // tile p: V[key 16p + r][32c + 8g .. +7], c = 0..3
 };
 
+// Page numbers of the two 16-key tiles of the pair at t0 (wave-uniform: a
+// 16-key tile lies inside one page since block_size >= 16 and tiles are
+// aligned to 16), from the workgroup's LDS copy of its page-table range,
+// clamped into the pool.  Keys past L use the page of key L - 1.
+__device__ __forceinline__ void pair_pages(const int* s_pages, int page0, int t0, int L, int log2_bs,
+                                           int64_t num_blocks, int64_t& blk0, int64_t& blk1) {
+  const int tile0 = __builtin_amdgcn_readfirstlane(min(t0, L - 1));
+  const int tile1 = __builtin_amdgcn_readfirstlane(min(t0 + 16, L - 1));
+  blk0 = __builtin_amdgcn_readfirstlane(s_pages[(tile0 >> log2_bs) - page0]);
+  blk1 = __builtin_amdgcn_readfirstlane(s_pages[(tile1 >> log2_bs) - page0]);
+  blk0 = blk0 < 0 ? 0 : (blk0 >= num_blocks ? num_blocks - 1 : blk0);  // never leave the pool
+  blk1 = blk1 < 0 ? 0 : (blk1 >= num_blocks ? num_blocks - 1 : blk1);
+}
+
+// K and V of the pair at t0 whose tiles lie in pages blk0, blk1.  Keys past
+// L re-read key L - 1: their probabilities are exactly 0 and the cache rows
+// below L hold finite values, so they add nothing.
 __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict__ k_cache,
-                                          const bf16_t* __restrict__ v_cache, const int* s_pages, int page0, int t0,
+                                          const bf16_t* __restrict__ v_cache, int64_t blk0, int64_t blk1, int t0,
                                           int L, int kvh, int KV, int log2_bs, int r, int g) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    // A 16-key tile lies inside one page (block_size >= 16, tiles aligned to
-    // 16), so its page number is wave-uniform; it comes from the workgroup's
-    // copy of its page-table range in LDS, so no global table lookup sits
-    // between a step and the loads it prefetches.  Keys past L re-read key
-    // L - 1: their probabilities are exactly 0 and the cache rows below L
-    // hold finite values, so they add nothing.
-    const int tile = __builtin_amdgcn_readfirstlane(min(t0 + 16 * p, L - 1));
-    const int64_t blk = __builtin_amdgcn_readfirstlane(s_pages[(tile >> log2_bs) - page0]);
-    const int64_t page = (blk << log2_bs) * KV * kD;  // wave-uniform
+    const int64_t page = ((p ? blk1 : blk0) << log2_bs) * KV * kD;  // wave-uniform
     const uint32_t tok = (uint32_t)min(t0 + 16 * p + r, L - 1);
     const uint32_t off = ((tok & ((1u << log2_bs) - 1)) * (uint32_t)KV + (uint32_t)kvh) * kD;
     const bf16_t* ks = k_cache + page + off + 32 * g;
@@ -125,7 +134,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = H / KV, R = S * G;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, so its addressing is scalar
   const int r = lane & 15, g = lane >> 4;
 
   // Fused: 32 jobs of one 128-element row on 16 lanes -- q rows [0, R), then
@@ -158,10 +168,10 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     f_w8 = ld128((f_jj < f_jk ? ra.q_weight : ra.k_weight) + f_s16 * 8);
     f_slot = ra.slots[tok];
     f_trow = ra.positions[tok];
-    f_trow = f_trow < 0 ? 0 : (f_trow >= ra.table_rows ? ra.table_rows - 1 : f_trow);
   }
 
   const int L = min(seq_lens[b], max_seq_len);  // max_seq_len <= table span, checked on the host
+
   // This workgroup's keys: split `split` of [0, L), in whole 32-key pairs.
   const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
   const int t_begin = split * span;
@@ -169,21 +179,54 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   const bool single = L <= span;  // the whole context is in split 0
   if (single && split > 0) return;
   const int32_t* table_row = block_table + (int64_t)b * table_stride;
-  // This split's page numbers (clamped into the pool) into LDS.
+
+  // This split's page numbers (as stored; clamped when read), staged into LDS below.  One entry per thread
+  // covers spans up to 512 pages; the load is unconditional (an empty split
+  // reads entry 0) so the waits below count exactly.
   const int page0 = t_begin >> log2_bs;
   const int npages = t_end > t_begin ? ((t_end - 1) >> log2_bs) - page0 + 1 : 0;  // <= kMaxSpanPages (host check)
-  for (int i = tid; i < npages; i += 64 * kWaves) {
-    const int64_t blk = table_row[page0 + i];
-    s_pages[i] = (int)(blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk));  // never leave the pool
+  const int64_t my_page = table_row[npages > 0 ? page0 + min(tid, npages - 1) : 0];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The waves take pairs wave, wave + 8, ... so at any time the workgroup reads
+  // 8 neighbouring pairs of the same pages.  Each wave's first pair is requested
+  // right away, its pages read straight from the table, so it is in flight
+  // during the page-table staging, the fused q/k work and the barrier.
+  const int stride = 32 * kWaves;
+  const int t_first = t_begin + 32 * wave;
+  const int n = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
+  // (Issued by every wave -- a wave without pairs reads a valid row it never
+  // uses -- so that no branch blurs the wait counts that follow.)
+  PairRegs kv_a, kv_b;
+  u32x4 f_c8 = {0u, 0u, 0u, 0u}, f_s8 = {0u, 0u, 0u, 0u};
+  {
+    const int Lc = L > 0 ? L : 1;  // an empty context still addresses key 0
+    const int tile0 = min(t_first, Lc - 1), tile1 = min(t_first + 16, Lc - 1);
+    const int e0 = table_row[tile0 >> log2_bs], e1 = table_row[tile1 >> log2_bs];  // both requested before either is used
+    const int nb = (int)num_blocks;  // < 2^31, checked on the host
+    const int64_t blk0 = e0 < 0 ? 0 : (e0 >= nb ? nb - 1 : e0);  // never leave the pool
+    const int64_t blk1 = e1 < 0 ? 0 : (e1 >= nb ? nb - 1 : e1);
+    // Fused: the RoPE row of each new token's position, requested while the
+    // first pair's page numbers are on their way.
+    if constexpr (kFused) {
+      f_trow = f_trow < 0 ? 0 : (f_trow >= ra.table_rows ? ra.table_rows - 1 : f_trow);
+      f_c8 = ld128(ra.cos_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
+      f_s8 = ld128(ra.sin_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
+    }
+    load_pair(kv_a, k_cache, v_cache, blk0, blk1, t_first, Lc, kvh, KV, log2_bs, r, g);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // (Every thread writes its entry, past npages too -- never read -- so the
+  // load above is not moved into a branch.)
+  s_pages[tid] = (int)my_page;
+  for (int i = tid + 64 * kWaves; i < npages; i += 64 * kWaves) {  // spans beyond 512 pages
+    s_pages[i] = table_row[page0 + i];
   }
 
   if constexpr (kFused) {
-    // The new tokens' rows, computed now that the table row of each position
-    // has arrived (its load was issued with the rows'); see the top of the
-    // kernel for the job layout.
-    const u32x4 c8 = ld128(ra.cos_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
-    const u32x4 sn8 = ld128(ra.sin_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
-    const u32x4 normed = norm_rope_16v(f_raw, f_w8, c8, sn8, ra.eps, f_s16);
+    // The new tokens' rows (see the top of the kernel for the job layout).
+    const u32x4 normed = norm_rope_16v(f_raw, f_w8, f_c8, f_s8, ra.eps, f_s16);
     if (f_job < f_jk) {
       s_q[f_jj][f_s16] = normed;
     } else if (f_job < f_jend) {
@@ -235,9 +278,6 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The waves take pairs wave, wave + 8, ... so at any time the workgroup reads
-  // 8 neighbouring pairs of the same pages.
-  const int stride = 32 * kWaves;
   auto step = [&](PairRegs& cur, const int t0) {
     if constexpr (kFused) {
       if (t0 + 31 >= L - S) {  // wave-uniform: the pair holds new tokens, whose rows come from LDS
@@ -316,20 +356,19 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   // issued unconditionally (past the wave's last pair it re-reads that pair,
   // an L2 hit), so the only branch skips a compute step and the vmcnt wait
   // before each step counts exactly the 16 loads issued after its own.
-  const int t_first = t_begin + 32 * wave;
-  const int n = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
   if (n > 0) {
     const int t_last = t_first + (n - 1) * stride;
-    PairRegs ra, rb;
-    load_pair(ra, k_cache, v_cache, s_pages, page0, t_first, L, kvh, KV, log2_bs, r, g);
     for (int i = 0; i < n; i += 2) {
       const int ta = t_first + i * stride;
-      load_pair(rb, k_cache, v_cache, s_pages, page0, min(ta + stride, t_last), L, kvh, KV, log2_bs, r, g);
+      int64_t blk0, blk1;
+      pair_pages(s_pages, page0, min(ta + stride, t_last), L, log2_bs, num_blocks, blk0, blk1);
+      load_pair(kv_b, k_cache, v_cache, blk0, blk1, min(ta + stride, t_last), L, kvh, KV, log2_bs, r, g);
       __builtin_amdgcn_sched_barrier(0);
-      step(ra, ta);
-      load_pair(ra, k_cache, v_cache, s_pages, page0, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, r, g);
+      step(kv_a, ta);
+      pair_pages(s_pages, page0, min(ta + 2 * stride, t_last), L, log2_bs, num_blocks, blk0, blk1);
+      load_pair(kv_a, k_cache, v_cache, blk0, blk1, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, r, g);
       __builtin_amdgcn_sched_barrier(0);
-      if (i + 1 < n) step(rb, ta + stride);
+      if (i + 1 < n) step(kv_b, ta + stride);
     }
   }
 
@@ -447,7 +486,7 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   OXR_RETURN_IF((!ra && !q) || !k_cache || !v_cache || !seq_lens || !block_table || !out, OXR_ERR_INVALID_ARG);
   const size_t need = oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
-  OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535 || num_blocks > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
   const int splits = splits_for(batch, num_kv_heads);
   {
     // One split's page-table range must fit the kernel's LDS copy.
