@@ -413,37 +413,51 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 // Merge of the context splits of every (sequence, kv head): one workgroup per
 // pair, one thread per 4 output dims of a row.  Sequences whose context fitted
 // one split were already stored by the main kernel.
-__global__ __launch_bounds__(256) void paged_extend_merge_kernel(const float* __restrict__ part_o,
-                                                                 const float* __restrict__ part_ml,
-                                                                 const int32_t* __restrict__ seq_lens, int S, int H,
-                                                                 int KV, int max_seq_len, int splits,
-                                                                 bf16_t* __restrict__ out) {
+__global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(const float* __restrict__ part_o,
+                                                                          const float* __restrict__ part_ml,
+                                                                          const int32_t* __restrict__ seq_lens, int S,
+                                                                          int H, int KV, int max_seq_len, int splits,
+                                                                          bf16_t* __restrict__ out) {
+  constexpr int kChunk = 8;  // splits whose partials are requested together
   const int kvh = blockIdx.x, b = blockIdx.y;
+  const int G = H / KV;
+  // One thread per 4 output dims of a row (blockDim = rows * 32).
+  const int rr = threadIdx.x / (kD / 4), d0 = (threadIdx.x % (kD / 4)) * 4;
+  const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
+  float m = -INFINITY, l = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < splits; c0 += kChunk) {
+    // The chunk's partials are requested together; entries past the last
+    // split re-read it and enter with weight 0 (max -inf), exactly neutral.
+    f32x2 ml[kChunk];
+    f32x4 v[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const int64_t u = unit0 + min(c0 + j, splits - 1);
+      ml[j] = *reinterpret_cast<const f32x2*>(part_ml + (u * kRows + rr) * 2);
+      v[j] = *reinterpret_cast<const f32x4*>(part_o + (u * kRows + rr) * kD + d0);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const float mj = c0 + j < splits ? ml[j][0] : -INFINITY;
+      const float mn = fmaxf(m, mj);
+      const float mu = (mn == -INFINITY) ? 0.f : mn;
+      const float a = exp2f(m - mu), w = exp2f(mj - mu);
+      l = l * a + ml[j][1] * w;
+      acc = acc * a + v[j] * w;
+      m = mn;
+    }
+  }
+  // Sequences whose context fitted one split were stored by the main kernel
+  // (checked only now, so the partials above were requested without waiting).
   const int L = min(seq_lens[b], max_seq_len);
   const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
   if (L <= span) return;
-  const int G = H / KV, R = S * G;
-  const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
-  for (int idx = threadIdx.x; idx < R * (kD / 4); idx += blockDim.x) {
-    const int rr = idx / (kD / 4), d0 = (idx % (kD / 4)) * 4;
-    float m = -INFINITY, l = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < splits; ++c) {
-      const f32x2 ml = *reinterpret_cast<const f32x2*>(part_ml + ((unit0 + c) * kRows + rr) * 2);
-      const f32x4 v = *reinterpret_cast<const f32x4*>(part_o + ((unit0 + c) * kRows + rr) * kD + d0);
-      const float mn = fmaxf(m, ml[0]);
-      const float mu = (mn == -INFINITY) ? 0.f : mn;
-      const float a = exp2f(m - mu), w = exp2f(ml[0] - mu);
-      l = l * a + ml[1] * w;
-      acc = acc * a + v * w;
-      m = mn;
-    }
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    const int s = rr / G, hh = rr % G;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
-    dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
-    dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
-  }
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const int s = rr / G, hh = rr % G;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
+  dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
+  dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
 }
 
 // Context splits per (sequence, kv head): about one 8-wave workgroup per CU
@@ -510,7 +524,8 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   }
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;
-  hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(256), 0, s, part_o, part_ml,
+  const int rows = tokens_per_seq * (num_heads / num_kv_heads);
+  hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(rows * kD / 4), 0, s, part_o, part_ml,
                      seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, out);
   return OXR_LAUNCH_STATUS();
 }
