@@ -87,32 +87,45 @@ def step_bytes(config, batch, tokens_per_seq, kv_lens_mean) -> dict:
     return {"weights": weights, "kv_read": kv_read, "kv_write": kv_write, "total": weights + kv_read + kv_write}
 
 
-def time_attention(config, cache, loop, iters: int = 50) -> dict:
-    """The dominant kernel (paged verify attention, one fused launch) at the step's layer shape,
-    timed with HIP events on the stream it is launched on."""
+def time_attention(config, model, cache, loop, iters: int = 56) -> dict:
+    """The dominant kernel: the layer's fused attention launch (q/k norm + RoPE + K/V store + paged
+    verify attention, then the split merge) at the step's shape, timed with HIP events on the stream it
+    is launched on.  Launches rotate over the layers' caches, so the K/V comes from HBM as in the step."""
     b, s = loop.batch, loop.tokens_per_seq
+    c, w = config, model.weights
     seq = (loop.seq_len + s).to(torch.int32)
     g = torch.Generator(device="cuda").manual_seed(5)
-    q = torch.randn(b, s, config.num_heads, config.head_dim, generator=g, device="cuda").to(torch.bfloat16)
-    out = torch.empty_like(q)
-    max_seq_len = loop.block_table.shape[1] * cache.block_size
-    ws = torch.zeros(attention.workspace_bytes(b, config.num_kv_heads, max_seq_len), dtype=torch.uint8, device="cuda")
-    run = lambda: attention.paged_extend(q, cache.k[0], cache.v[0], seq, loop.block_table, max_seq_len=max_seq_len,
-                                         out=out, workspace=ws)
-    for _ in range(5):
-        run()
+    qkv = (torch.randn(b * s, c.qkv_size, generator=g, device="cuda")).to(torch.bfloat16)
+    pos = (seq.to(torch.int64)[:, None] - s + torch.arange(s, device="cuda")[None, :]).reshape(-1)
+    bs = cache.block_size
+    table = loop.block_table.to(torch.int64)
+    slots = (table.gather(1, (pos.view(b, s) // bs)) * bs + pos.view(b, s) % bs).reshape(-1)
+    out = torch.empty(b, s, c.num_heads, c.head_dim, dtype=torch.bfloat16, device="cuda")
+    max_seq_len = loop.block_table.shape[1] * bs
+    ws = torch.zeros(attention.workspace_bytes(b, c.num_kv_heads, max_seq_len), dtype=torch.uint8, device="cuda")
+
+    def run(i):
+        layer = w.layers[i % c.num_layers]
+        attention.qk_norm_rope_paged_extend(
+            qkv, layer.q_norm, layer.k_norm, w.rope_cos, w.rope_sin, pos, float(c.rms_norm_eps),
+            cache.k[i % c.num_layers], cache.v[i % c.num_layers], slots, seq, loop.block_table, c.num_heads,
+            scale=c.head_dim ** -0.5, max_seq_len=max_seq_len, out=out, workspace=ws)
+
+    for i in range(c.num_layers):
+        run(i)
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(iters):
-        run()
+    for i in range(iters):
+        run(i)
     end.record(stream)
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1000.0 / iters
-    kv = int(seq.sum().item()) * 2 * 2 * config.num_kv_heads * config.head_dim
-    qo = 2 * 2 * b * s * config.num_heads * config.head_dim
-    return {"us": us, "bytes": kv + qo}
+    kv_token = 2 * 2 * c.num_kv_heads * c.head_dim
+    kv = int(seq.sum().item()) * kv_token  # every visible key and value read once
+    io = 2 * b * s * (c.qkv_size + c.num_heads * c.head_dim) + b * s * kv_token  # qkv in, out, new K/V rows
+    return {"us": us, "bytes": kv + io}
 
 
 COPY_BYTES = 256 << 20  # calibration copy for the FETCH_SIZE / WRITE_SIZE counters
@@ -131,10 +144,10 @@ def measured_traffic() -> int | None:
     return None
 
 
-def pmc_driver(config, cache, loop) -> None:
+def pmc_driver(config, model, cache, loop) -> None:
     """Ten attention launches at the step's shape, then five device copies of COPY_BYTES: the
     workload of the committed FETCH_SIZE / WRITE_SIZE runs."""
-    time_attention(config, cache, loop, iters=10)
+    time_attention(config, model, cache, loop, iters=10)
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(5):
@@ -222,7 +235,7 @@ def main() -> int:
                                    table_width=width, device=device)
     loop.load(histories, seq_lens, table)
     if args.pmc_driver:
-        pmc_driver(config, cache, loop)
+        pmc_driver(config, model, cache, loop)
         return 0
     log("capturing graph")
     loop.capture()
@@ -250,7 +263,7 @@ def main() -> int:
     step_gbs = traffic["total"] / (ms * 1e-3) / 1e9
     log(f"{ms * 1000:.1f} us/step, {committed} tokens committed, step HBM {step_gbs:.0f} GB/s")
 
-    attn = time_attention(config, cache, loop)
+    attn = time_attention(config, model, cache, loop)
     attn_gbs = attn["bytes"] / (attn["us"] * 1e-6) / 1e9
     log(f"attention kernel {attn['us']:.2f} us, {attn_gbs:.0f} GB/s")
 
@@ -285,7 +298,8 @@ def main() -> int:
         "accepted_drafts_per_step": accepted_drafts / args.steps,
         "step_roofline": {"bound": "hbm", "bytes": traffic["total"], "achieved": step_gbs, "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
-        "roofline": {"kernel": "paged verify attention, one layer (paged_extend_kernel + paged_extend_merge_kernel)",
+        "roofline": {"kernel": "fused verify attention launch, one layer (paged_extend_kernel<true> + "
+                               "paged_extend_merge_kernel)",
                      "bound": "hbm", "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": attn_gbs / HBM_PEAK_GBS, "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"],
                      "traffic": measured_traffic()},
