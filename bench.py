@@ -60,7 +60,8 @@ def build_workload(args, device):
     width = -(-max_len // bs)
     num_blocks = args.batch * width + 16
     weights = language.random_weights(config, max_len + 64, seed=args.seed, device=device)
-    model = language.LanguageModel(config, weights)
+    model = language.LanguageModel(config, weights)  # packs the GEMM weights
+    del weights
     cache = kv_cache.KVCache(config.num_layers, config.num_kv_heads, config.head_dim, num_blocks, block_size=bs)
     g = torch.Generator(device=device).manual_seed(args.seed + 1)
     for layer in range(config.num_layers):  # context K/V ~N(0, 1), as keys after the q/k norm
@@ -162,7 +163,7 @@ def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    weights = model.weights.to("cpu")
+    weights = model.weights.unpacked().to("cpu")
     # Compact copy of the pages the batch uses (the GPU pool holds many more).
     used = np.unique(table)
     remap = np.zeros(int(used.max()) + 1, dtype=np.int32)

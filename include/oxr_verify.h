@@ -254,6 +254,29 @@ int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight
                        oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes,
                        oxr_stream_t stream);
 
+/*
+ * (4c) Packed weights.  The reference keeps nn.Linear weights row-major
+ * ([rows, k], language.py:234-245 and the LM head of :213-214); these entry
+ * points take the same weights re-ordered once, at load time, into the order
+ * the GEMM kernels consume them: for each 16-row tile t and 128-column step q,
+ * four contiguous 1 KiB blocks, block i holding, for lane l = 16g + r,
+ * w[16t + r][128q + 32i + 8g .. +8).  Every load instruction of the kernels
+ * then reads 1 KiB of contiguous memory.  The last tile is zero-padded, so a
+ * packed weight holds oxr_packed_weight_elems(rows, k) bf16 elements.
+ * The *_packed GEMM entries behave exactly like their row-major versions
+ * (same requirements, bit-identical results) given oxr_pack_weight_bf16 of
+ * the same weight; OXR_EPI_SILU_MUL additionally needs n % 16 == 0.
+ */
+size_t oxr_packed_weight_elems(int64_t rows, int64_t k);
+int oxr_pack_weight_bf16(const oxr_bf16* w, int64_t rows, int64_t k, oxr_bf16* packed, oxr_stream_t stream);
+int oxr_gemm_bf16_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed, int64_t k, int64_t n,
+                         int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream);
+int oxr_gemm_bf16_partial_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed, int64_t k,
+                                 int64_t n, float* partials, int32_t k_splits, oxr_stream_t stream);
+int oxr_lm_head_argmax_packed(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight_packed, int64_t hidden_size,
+                              int64_t vocab, oxr_bf16* logits, int64_t* predicted, void* workspace,
+                              size_t workspace_bytes, oxr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

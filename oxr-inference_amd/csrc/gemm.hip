@@ -6,14 +6,22 @@
 //
 // * A workgroup owns one tile of 16 * NA weight rows (output columns), all
 //   M <= 16 * NB token rows, and one of `k_splits` slices of K; its WAVES
-//   waves split that slice further.  A wave walks its k range in 128-k steps:
-//   a lane loads 64 contiguous bytes of a weight row, which is exactly its
-//   A-operand fragment of v_mfma_f32_16x16x32_bf16 (lane (r, g) holds
-//   W[row r][k + 32g .. 32g + 31], i.e. four MFMA k-steps), and the X
-//   fragments with the same k-slot mapping (X is at most 64 rows and stays in
-//   L2).  Step i + 1's W and X are in flight while step i is multiplied; there
-//   are no dependent loads in the loop, so the in-order vmcnt waits only ever
-//   wait for the step being consumed.
+//   waves split that slice further.  A wave walks its k range in 128-k steps
+//   of four load instructions per 16-row tile: instruction i brings lane
+//   (r, g) W[row r][k + 32i + 8g, +8), its A-operand fragment of
+//   v_mfma_f32_16x16x32_bf16 for k-step i, and the X fragments follow the
+//   same mapping (X is at most 64 rows and stays in L2).  Step i + 1's W and
+//   X are in flight while step i is multiplied; there are no dependent loads
+//   in the loop, so the in-order vmcnt waits only ever wait for the step
+//   being consumed.
+// * What bounds these kernels is the vector memory pipeline's rate over cache
+//   lines, not HBM bytes: an instruction of the row-major mapping touches 16
+//   rows' worth of lines.  Weights may therefore come pre-packed (PW, written
+//   once by oxr_pack_weight_bf16): for every 16-row tile t and 128-k step q,
+//   four contiguous 1 KiB blocks, block i holding the fragments of k-step i in
+//   lane order (lane 16g + r: W[16t + r][128q + 32i + 8g, +8)), so each load
+//   instruction reads 1 KiB of contiguous memory.  Same arithmetic, same
+//   order: packed and row-major results are bit-identical.
 // * The waves' fp32 tiles are summed in LDS in a fixed order, then the
 //   epilogue runs on the finished tile:
 //     kStore        Y = bf16(acc)
@@ -79,7 +87,7 @@ struct Stage {
   u32x4 x[NB][4];
 };
 
-template <int NA, int NB, int EPI, int WAVES>
+template <int NA, int NB, int EPI, int WAVES, bool PW>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
   constexpr int kTileRows = 16 * NA;                          // output columns of this workgroup
   constexpr int kLoadTiles = (EPI == kSiluMul) ? 2 * NA : NA;  // gate + up tiles for kSiluMul
@@ -93,22 +101,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
   const int64_t k_per_wave = k_slice / WAVES;
   const int64_t k_begin = blockIdx.y * k_slice + wave * k_per_wave, k_end = k_begin + k_per_wave;
 
-  // Weight row pointers of this lane, one per loaded tile (rows past N clamp
-  // to the last row; their results are dropped).
+  // Weight pointers of this lane, one per loaded tile (rows past N clamp to
+  // the last row, or tile, whose results are dropped).  Packed: the lane's
+  // fragment of the tile's first block; step k's block i is at + 16k + 512i.
   const bf16_t* wrow[kLoadTiles];
 #pragma unroll
   for (int a = 0; a < kLoadTiles; ++a) {
     int64_t row = n0 + 16 * (a % NA) + r;
     row = row < args.N ? row : args.N - 1;
     if (EPI == kSiluMul && a >= NA) row += args.N;
-    wrow[a] = args.w + row * K + 32 * g;
+    wrow[a] = PW ? args.w + (row >> 4) * (K * 16) + lane * 8 : args.w + row * K + 8 * g;
   }
   // Token rows past M read row 0 and multiply into accumulators nobody stores.
   const bf16_t* xrow[NB];
 #pragma unroll
   for (int bt = 0; bt < NB; ++bt) {
     const int tok = 16 * bt + r;
-    xrow[bt] = args.x + (int64_t)(tok < args.M ? tok : 0) * args.ldx + 32 * g;
+    xrow[bt] = args.x + (int64_t)(tok < args.M ? tok : 0) * args.ldx + 8 * g;
   }
 
   f32x4 acc[kLoadTiles][NB];
@@ -121,11 +130,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
 #pragma unroll
     for (int a = 0; a < kLoadTiles; ++a)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st.w[a][i] = ld128(wrow[a] + k + 8 * i);
+      for (int i = 0; i < 4; ++i) st.w[a][i] = ld128(PW ? wrow[a] + 16 * k + 512 * i : wrow[a] + k + 32 * i);
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st.x[bt][i] = ld128(xrow[bt] + k + 8 * i);
+      for (int i = 0; i < 4; ++i) st.x[bt][i] = ld128(xrow[bt] + k + 32 * i);
   };
 
   auto compute = [&](const Stage<kLoadTiles, NB>& st) {
@@ -314,13 +323,13 @@ constexpr int kLmDepth = 4;          // weight stages in flight per wave
 constexpr int kLmMaxK = 2048;        // X in LDS: NB * 16 * K * 2 bytes <= 128 KB
 constexpr int kLmStageThreads = 64 * kLmWaves;
 
-template <int NB, int K>
+template <int NB, int K, bool PW>
 __global__ __launch_bounds__(64 * kLmWaves) void lm_head_lds_kernel(const bf16_t* __restrict__ x, int64_t ldx, int M,
                                                                    const bf16_t* w, int64_t N,
                                                                    bf16_t* __restrict__ logits, int64_t ldl,
                                                                    uint64_t* __restrict__ best_out) {
   static_assert(K % (kKStep * kLmDepth) == 0 && K <= kLmMaxK, "unsupported hidden size");
-  // xs[((q * 4 + i) * NB + bt) * 64 + lane] = X[16 bt + lane % 16][128 q + 32 (lane / 16) + 8 i, +8): the B
+  // xs[((q * 4 + i) * NB + bt) * 64 + lane] = X[16 bt + lane % 16][128 q + 32 i + 8 (lane / 16), +8): the B
   // fragment of MFMA i of k-stage q for token tile bt, matching the weight fragments' k-slot mapping.
   extern __shared__ u32x4 xs[];
   __shared__ uint64_t wave_best[kLmWaves][NB * 16];
@@ -339,12 +348,13 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_lds_kernel(const bf16_t
     s = s > 0 ? s : 0;  // a wave without tiles reads (and never uses) the last weight row
     int64_t row = (gw + (s / ksteps) * nw) * 16 + r;
     row = row < N ? row : N - 1;
-    return w + row * K + (s % ksteps) * kKStep + 32 * g;
+    if constexpr (PW) return w + (row >> 4) * (K * 16) + (s % ksteps) * (16 * kKStep) + lane * 8;
+    return w + row * K + (s % ksteps) * kKStep + 8 * g;
   };
   auto load = [&](u32x4 (&dst)[4], int64_t s) {
     const bf16_t* p = stage_ptr(s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = ld128(p + 8 * i);
+    for (int i = 0; i < 4; ++i) dst[i] = ld128(p + (PW ? 512 * i : 32 * i));
   };
 
   // 1. X rows into registers (unconditional: indices past the end re-read the last chunk), then the first
@@ -369,7 +379,7 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_lds_kernel(const bf16_t
   for (int c = 0; c < kChunks; ++c) {
     const int idx = threadIdx.x + c * kLmStageThreads;
     const int m = idx / (K / 8), k = (idx % (K / 8)) * 8;
-    const int q = k / kKStep, kk = k % kKStep, gg = kk / 32, ii = (kk % 32) / 8;
+    const int q = k / kKStep, kk = k % kKStep, ii = kk / 32, gg = (kk % 32) / 8;
     xs[((q * 4 + ii) * NB + m / 16) * 64 + gg * 16 + (m % 16)] = xr[c];
   }
   __syncthreads();
@@ -452,32 +462,32 @@ int device_cus() {
   return cached[dev];
 }
 
-template <int NB, int K>
+template <int NB, int K, bool PW>
 int launch_lm_head_lds(const bf16_t* x, int64_t ldx, int M, const bf16_t* w, int64_t N, bf16_t* logits,
                        uint64_t* best, int grid, hipStream_t s) {
   constexpr size_t lds = (size_t)NB * 16 * K * sizeof(bf16_t);
   static bool attr_set = false;  // per instantiation; setting it twice is harmless
   if (!attr_set) {
-    const hipError_t e =
-        hipFuncSetAttribute((const void*)lm_head_lds_kernel<NB, K>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t e = hipFuncSetAttribute((const void*)lm_head_lds_kernel<NB, K, PW>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((lm_head_lds_kernel<NB, K>), dim3((unsigned)grid), dim3(64 * kLmWaves), lds, s, x, ldx, M, w, N,
-                     logits, N, best);
+  hipLaunchKernelGGL((lm_head_lds_kernel<NB, K, PW>), dim3((unsigned)grid), dim3(64 * kLmWaves), lds, s, x, ldx, M, w,
+                     N, logits, N, best);
   return OXR_LAUNCH_STATUS();
 }
 
 // Hidden sizes with a persistent LM-head instantiation (X of up to 32 rows fits LDS).
 bool lm_head_lds_supported(int64_t m, int64_t k) { return m <= 32 && (k == 512 || k == 1024 || k == 2048); }
 
-template <int NB>
+template <int NB, bool PW>
 int launch_lm_head_lds_k(const bf16_t* x, int64_t ldx, int M, const bf16_t* w, int64_t K, int64_t N, bf16_t* logits,
                          uint64_t* best, int grid, hipStream_t s) {
   switch (K) {
-    case 512: return launch_lm_head_lds<NB, 512>(x, ldx, M, w, N, logits, best, grid, s);
-    case 1024: return launch_lm_head_lds<NB, 1024>(x, ldx, M, w, N, logits, best, grid, s);
-    case 2048: return launch_lm_head_lds<NB, 2048>(x, ldx, M, w, N, logits, best, grid, s);
+    case 512: return launch_lm_head_lds<NB, 512, PW>(x, ldx, M, w, N, logits, best, grid, s);
+    case 1024: return launch_lm_head_lds<NB, 1024, PW>(x, ldx, M, w, N, logits, best, grid, s);
+    case 2048: return launch_lm_head_lds<NB, 2048, PW>(x, ldx, M, w, N, logits, best, grid, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
@@ -488,51 +498,55 @@ struct LaunchConfig {
   int k_splits;  // k slices across workgroups (kPartial only)
 };
 
-template <int NA, int NB, int EPI, int WAVES>
+template <int NA, int NB, int EPI, int WAVES, bool PW>
 int launch_gemm(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   const int64_t tiles = (a.N + 16 * NA - 1) / (16 * NA);
-  hipLaunchKernelGGL((gemm_kernel<NA, NB, EPI, WAVES>), dim3((unsigned)tiles, (unsigned)c.k_splits), dim3(64 * WAVES),
-                     0, s, a);
+  hipLaunchKernelGGL((gemm_kernel<NA, NB, EPI, WAVES, PW>), dim3((unsigned)tiles, (unsigned)c.k_splits),
+                     dim3(64 * WAVES), 0, s, a);
   return OXR_LAUNCH_STATUS();
 }
 
-template <int NA, int EPI, int WAVES>
+template <int NA, int EPI, int WAVES, bool PW>
 int dispatch_nb(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   switch ((a.M + 15) / 16) {
-    case 1: return launch_gemm<NA, 1, EPI, WAVES>(a, c, s);
-    case 2: return launch_gemm<NA, 2, EPI, WAVES>(a, c, s);
-    case 3: return launch_gemm<NA, 3, EPI, WAVES>(a, c, s);
-    case 4: return launch_gemm<NA, 4, EPI, WAVES>(a, c, s);
+    case 1: return launch_gemm<NA, 1, EPI, WAVES, PW>(a, c, s);
+    case 2: return launch_gemm<NA, 2, EPI, WAVES, PW>(a, c, s);
+    case 3: return launch_gemm<NA, 3, EPI, WAVES, PW>(a, c, s);
+    case 4: return launch_gemm<NA, 4, EPI, WAVES, PW>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
-template <int NA, int EPI>
+template <int NA, int EPI, bool PW>
 int dispatch_waves(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   switch (c.waves) {
-    case 1: return dispatch_nb<NA, EPI, 1>(a, c, s);
-    case 2: return dispatch_nb<NA, EPI, 2>(a, c, s);
-    case 4: return dispatch_nb<NA, EPI, 4>(a, c, s);
-    case 8: return dispatch_nb<NA, EPI, 8>(a, c, s);
+    case 1: return dispatch_nb<NA, EPI, 1, PW>(a, c, s);
+    case 2: return dispatch_nb<NA, EPI, 2, PW>(a, c, s);
+    case 4: return dispatch_nb<NA, EPI, 4, PW>(a, c, s);
+    case 8: return dispatch_nb<NA, EPI, 8, PW>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
 template <int EPI>
-int dispatch(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
-  switch (c.na) {
-    case 1: return dispatch_waves<1, EPI>(a, c, s);
-    case 2: return dispatch_waves<2, EPI>(a, c, s);
+int dispatch(const GemmArgs& a, const LaunchConfig& c, bool packed, hipStream_t s) {
+  switch (c.na * 2 + (packed ? 1 : 0)) {
+    case 2: return dispatch_waves<1, EPI, false>(a, c, s);
+    case 3: return dispatch_waves<1, EPI, true>(a, c, s);
+    case 4: return dispatch_waves<2, EPI, false>(a, c, s);
+    case 5: return dispatch_waves<2, EPI, true>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
-// Launch shape, from a sweep of the verify shapes on MI355X (M = 32):
-// weights with fp32-partial output (o_proj, down_proj: 2048 columns) take
-// 32-row tiles split over k until there are >= 256 workgroups of 4 waves;
-// others take 32-row tiles when that still gives >= 160 workgroups (gate_up,
-// LM head), else 16-row tiles (qkv), with 4 waves per workgroup (2 when there
-// are thousands of tiles, as in the LM head).
+// Launch shape, from a sweep of the verify shapes on MI355X (M = 32, packed
+// and row-major weights alike): 32-row tiles, or 16-row tiles when fewer than
+// 160 workgroups of 32 rows would remain (qkv); weights with fp32-partial
+// output (o_proj, down_proj: 2048 columns) split k until there are >= 256
+// workgroups; a workgroup's k slice goes to the fewest waves that leave each
+// at most 8 steps of 128 (o_proj: 1 wave; qkv, gate_up, down_proj: 2).  More
+// waves per workgroup only add requests in flight to an already saturated
+// memory pipeline (4 waves: gate_up 18.1 vs 15.7 us, down_proj 9.9 vs 8.5).
 LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
   LaunchConfig c{1, 1, 1};
   if (allow_k_splits) {
@@ -542,10 +556,8 @@ LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
   } else {
     c.na = (n_rows + 31) / 32 >= 160 ? 2 : 1;
   }
-  const int64_t tiles = (n_rows + 16 * c.na - 1) / (16 * c.na);
-  const int want_waves = tiles >= 2048 ? 2 : 4;
   const int64_t k_slice = K / c.k_splits;
-  while (c.waves < want_waves && k_slice % (2 * c.waves * kKStep) == 0) c.waves *= 2;
+  while (k_slice / c.waves > 8 * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 8) c.waves *= 2;
   return c;
 }
 
@@ -557,32 +569,41 @@ int check_common(const void* x, int64_t ldx, int64_t M, const void* w, int64_t K
   return OXR_OK;
 }
 
-}  // namespace
-}  // namespace oxr
+// Packed layout (see the top of this file): one thread per 16-byte fragment
+// of the output, in output order; rows past `rows` (the last tile's padding)
+// are zero.
+__global__ __launch_bounds__(256) void pack_weight_kernel(const bf16_t* __restrict__ w, int64_t rows, int64_t K,
+                                                          int64_t chunks, bf16_t* __restrict__ packed) {
+  const int64_t ksteps = K / kKStep;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(c & 63), r = lane & 15, g = lane >> 4;
+    const int64_t blk = c >> 6;
+    const int i = (int)(blk & 3);
+    const int64_t q = (blk >> 2) % ksteps, t = (blk >> 2) / ksteps;
+    const int64_t row = 16 * t + r;
+    const u32x4 v = row < rows ? ld128(w + row * K + q * kKStep + 32 * i + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(packed + c * 8) = v;
+  }
+}
 
-extern "C" int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
-                             int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream) {
-  using namespace oxr;
+int gemm_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n, int32_t epilogue,
+               oxr_bf16* y, int64_t ldy, bool packed, oxr_stream_t stream) {
   int st = check_common(x, ldx, m, w, k, n);
   if (st) return st;
   OXR_RETURN_IF(epilogue != kStore && epilogue != kSiluMul && epilogue != kAddResidual, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(!y || ldy < n || ldy % 4 != 0 || (uintptr_t)y % 8 != 0, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(packed && epilogue == kSiluMul && n % 16 != 0, OXR_ERR_UNSUPPORTED);  // up rows start a tile
   if (m == 0) return OXR_OK;
   GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
   const LaunchConfig c = choose_config(n, k, false);
-  if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, s);
-  if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, s);
-  return dispatch<kStore>(a, c, s);
+  if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, packed, s);
+  if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, packed, s);
+  return dispatch<kStore>(a, c, packed, s);
 }
 
-extern "C" int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k) {
-  return oxr::choose_config(n, k, true).k_splits;
-}
-
-extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k,
-                                     int64_t n, float* partials, int32_t k_splits, oxr_stream_t stream) {
-  using namespace oxr;
+int gemm_partial_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
+                       float* partials, int32_t k_splits, bool packed, oxr_stream_t stream) {
   int st = check_common(x, ldx, m, w, k, n);
   if (st) return st;
   OXR_RETURN_IF(!partials || (uintptr_t)partials % 16 != 0 || n % 4 != 0, OXR_ERR_INVALID_ARG);
@@ -590,18 +611,12 @@ extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, 
   OXR_RETURN_IF(k_splits != c.k_splits, OXR_ERR_INVALID_ARG);
   if (m == 0) return OXR_OK;
   GemmArgs a{x, ldx, (int)m, w, k, n, nullptr, 0, nullptr, partials};
-  return dispatch<kPartial>(a, c, (hipStream_t)stream);
+  return dispatch<kPartial>(a, c, packed, (hipStream_t)stream);
 }
 
-extern "C" size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab) {
-  if (m <= 0 || vocab <= 0) return 0;
-  return (size_t)((vocab + 15) / 16) * (size_t)m * sizeof(uint64_t);  // enough for 16-row tiles
-}
-
-extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size,
-                                  int64_t vocab, oxr_bf16* logits, int64_t* predicted, void* workspace,
-                                  size_t workspace_bytes, oxr_stream_t stream) {
-  using namespace oxr;
+int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
+                  oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes, bool packed,
+                  oxr_stream_t stream) {
   int st = check_common(hidden, hidden_size, m, weight, hidden_size, vocab);
   if (st) return st;
   OXR_RETURN_IF(!predicted, OXR_ERR_INVALID_ARG);
@@ -616,18 +631,90 @@ extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_b
   if (lm_head_lds_supported(m, hidden_size)) {
     const int64_t num_tiles = (vocab + 15) / 16;
     num_best = (int)std::min<int64_t>(device_cus(), num_tiles);
-    st = m <= 16 ? launch_lm_head_lds_k<1>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, best,
-                                           num_best, s)
-                 : launch_lm_head_lds_k<2>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, best,
-                                           num_best, s);
+    const int key = (m <= 16 ? 0 : 2) + (packed ? 1 : 0);
+    st = key == 0   ? launch_lm_head_lds_k<1, false>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits,
+                                                     best, num_best, s)
+         : key == 1 ? launch_lm_head_lds_k<1, true>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits,
+                                                    best, num_best, s)
+         : key == 2 ? launch_lm_head_lds_k<2, false>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits,
+                                                     best, num_best, s)
+                    : launch_lm_head_lds_k<2, true>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits,
+                                                    best, num_best, s);
   } else {
     GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, best, nullptr};
     const LaunchConfig c = choose_config(vocab, hidden_size, false);
     num_best = (int)((vocab + 16 * c.na - 1) / (16 * c.na));
-    st = dispatch<kArgmax>(a, c, s);
+    st = dispatch<kArgmax>(a, c, packed, s);
   }
   if (st) return st;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(best),
                      num_best, (int)m, predicted);
   return OXR_LAUNCH_STATUS();
+}
+
+}  // namespace
+}  // namespace oxr
+
+extern "C" size_t oxr_packed_weight_elems(int64_t rows, int64_t k) {
+  if (rows <= 0 || k <= 0) return 0;
+  return (size_t)((rows + 15) / 16 * 16) * (size_t)k;
+}
+
+extern "C" int oxr_pack_weight_bf16(const oxr_bf16* w, int64_t rows, int64_t k, oxr_bf16* packed,
+                                    oxr_stream_t stream) {
+  using namespace oxr;
+  OXR_RETURN_IF(rows <= 0 || k <= 0 || !w || !packed, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(k % kKStep != 0 || ((uintptr_t)w | (uintptr_t)packed) % 16 != 0, OXR_ERR_UNSUPPORTED);
+  const int64_t elems = (int64_t)oxr_packed_weight_elems(rows, k);
+  const uintptr_t wb = (uintptr_t)w, pb = (uintptr_t)packed;
+  OXR_RETURN_IF(wb < pb + 2 * (uintptr_t)elems && pb < wb + 2 * (uintptr_t)(rows * k), OXR_ERR_INVALID_ARG);  // overlap
+  const int64_t chunks = elems / 8;
+  const int64_t blocks = std::min<int64_t>((chunks + 255) / 256, 4096);
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, w, rows, k, chunks,
+                     packed);
+  return OXR_LAUNCH_STATUS();
+}
+
+extern "C" int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
+                             int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream) {
+  return oxr::gemm_entry(x, ldx, m, w, k, n, epilogue, y, ldy, false, stream);
+}
+
+extern "C" int oxr_gemm_bf16_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed, int64_t k,
+                                    int64_t n, int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream) {
+  return oxr::gemm_entry(x, ldx, m, w_packed, k, n, epilogue, y, ldy, true, stream);
+}
+
+extern "C" int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k) {
+  return oxr::choose_config(n, k, true).k_splits;
+}
+
+extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k,
+                                     int64_t n, float* partials, int32_t k_splits, oxr_stream_t stream) {
+  return oxr::gemm_partial_entry(x, ldx, m, w, k, n, partials, k_splits, false, stream);
+}
+
+extern "C" int oxr_gemm_bf16_partial_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed,
+                                            int64_t k, int64_t n, float* partials, int32_t k_splits,
+                                            oxr_stream_t stream) {
+  return oxr::gemm_partial_entry(x, ldx, m, w_packed, k, n, partials, k_splits, true, stream);
+}
+
+extern "C" size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab) {
+  if (m <= 0 || vocab <= 0) return 0;
+  return (size_t)((vocab + 15) / 16) * (size_t)m * sizeof(uint64_t);  // enough for 16-row tiles
+}
+
+extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size,
+                                  int64_t vocab, oxr_bf16* logits, int64_t* predicted, void* workspace,
+                                  size_t workspace_bytes, oxr_stream_t stream) {
+  return oxr::lm_head_entry(hidden, m, weight, hidden_size, vocab, logits, predicted, workspace, workspace_bytes, false,
+                            stream);
+}
+
+extern "C" int oxr_lm_head_argmax_packed(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight_packed,
+                                         int64_t hidden_size, int64_t vocab, oxr_bf16* logits, int64_t* predicted,
+                                         void* workspace, size_t workspace_bytes, oxr_stream_t stream) {
+  return oxr::lm_head_entry(hidden, m, weight_packed, hidden_size, vocab, logits, predicted, workspace,
+                            workspace_bytes, true, stream);
 }

@@ -29,6 +29,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib, attention, gemm, lm_head
+from .gemm import Weight
 from .kv_cache import KVCache
 
 
@@ -55,24 +56,35 @@ class LanguageConfig:
 QWEN_SYNTHETIC = LanguageConfig(2048, 6144, 28, 16, 8, 128, 1e-6, 1e6, 151_936)
 
 
+_MATRICES = ("qkv", "o", "gate_up", "down")
+
+
 @dataclass
 class LayerWeights:
     input_norm: torch.Tensor   # [hidden]
-    qkv: torch.Tensor          # [(H + 2KV) * D, hidden]  (q | k | v rows, language.py:237)
+    qkv: Weight                # [(H + 2KV) * D, hidden]  (q | k | v rows, language.py:237)
     q_norm: torch.Tensor       # [D]
     k_norm: torch.Tensor       # [D]
-    o: torch.Tensor            # [hidden, H * D]
+    o: Weight                  # [hidden, H * D]
     post_norm: torch.Tensor    # [hidden]
-    gate_up: torch.Tensor      # [2 * intermediate, hidden]  (gate rows then up rows, language.py:238)
-    down: torch.Tensor         # [hidden, intermediate]
+    gate_up: Weight            # [2 * intermediate, hidden]  (gate rows then up rows, language.py:238)
+    down: Weight               # [hidden, intermediate]
+
+    def _map(self, matrix) -> "LayerWeights":
+        return LayerWeights(**{f: matrix(getattr(self, f)) if f in _MATRICES else getattr(self, f)
+                               for f in LayerWeights.__dataclass_fields__})
 
 
 @dataclass
 class LanguageWeights:
+    """The decoder's weights.  GEMM matrices (the four per layer and the LM head) are row-major
+    ``torch.Tensor``s as a checkpoint holds them, or :class:`~.gemm.PackedWeight`s after
+    :meth:`packed` -- the form :class:`LanguageModel` runs on."""
+
     embed: torch.Tensor        # [vocab, hidden]
     layers: list[LayerWeights]
     final_norm: torch.Tensor   # [hidden]
-    lm_head: torch.Tensor      # [vocab, hidden]
+    lm_head: Weight            # [vocab, hidden]
     rope_cos: torch.Tensor     # [max_positions, D/2] bf16
     rope_sin: torch.Tensor
 
@@ -82,6 +94,18 @@ class LanguageWeights:
             mv(self.embed), [LayerWeights(*(mv(getattr(l, f)) for f in LayerWeights.__dataclass_fields__)) for l in self.layers],
             mv(self.final_norm), mv(self.lm_head), mv(self.rope_cos), mv(self.rope_sin),
         )
+
+    def _map_matrices(self, matrix) -> "LanguageWeights":
+        return LanguageWeights(self.embed, [l._map(matrix) for l in self.layers], self.final_norm, matrix(self.lm_head),
+                               self.rope_cos, self.rope_sin)
+
+    def packed(self) -> "LanguageWeights":
+        """Every GEMM matrix packed once on its GPU (``gemm.pack_weight``); other tensors shared."""
+        return self._map_matrices(lambda w: w if isinstance(w, gemm.PackedWeight) else gemm.pack_weight(w))
+
+    def unpacked(self) -> "LanguageWeights":
+        """Every GEMM matrix row-major again; other tensors shared."""
+        return self._map_matrices(lambda w: w.unpack() if isinstance(w, gemm.PackedWeight) else w)
 
 
 def rope_tables(config: LanguageConfig, max_positions: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -173,11 +197,14 @@ class StepBuffers:
 
 
 class LanguageModel:
-    """Verify forward (``extend``) and LM head of the decoder on gfx950 kernels."""
+    """Verify forward (``extend``) and LM head of the decoder on gfx950 kernels.
+
+    The GEMM matrices are packed once here (``weights.packed()``, a copy: drop the row-major
+    ``weights`` afterwards to free them); ``self.weights`` holds the packed set."""
 
     def __init__(self, config: LanguageConfig, weights: LanguageWeights):
         self.config = config
-        self.weights = weights
+        self.weights = weights.packed()
 
     def extend(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers | None = None) -> torch.Tensor:
         """``[B * S, hidden]``: the final-norm hidden state of every new token (language.py:201-211).

@@ -10,6 +10,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .gemm import PackedWeight, Weight
 
 MAX_ROWS = 64
 
@@ -19,15 +20,18 @@ def workspace_bytes(rows: int, vocab: int) -> int:
 
 
 def lm_head_argmax(
-    hidden: torch.Tensor, weight: torch.Tensor, *, return_logits: bool = False, predicted: torch.Tensor | None = None,
+    hidden: torch.Tensor, weight: Weight, *, return_logits: bool = False, predicted: torch.Tensor | None = None,
     logits: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
-    """hidden bf16 ``[n, hidden]``, weight bf16 ``[vocab, hidden]`` -> (int64 ``[n]`` greedy ids,
-    bf16 ``[n, vocab]`` logits when ``return_logits`` else None)."""
-    device = _lib.require_gpu(hidden, weight, name="lm_head_argmax")
-    _lib.require(hidden.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "bf16 operands required")
-    _lib.require(hidden.dim() == 2 and weight.dim() == 2 and hidden.shape[1] == weight.shape[1], "shape mismatch")
-    _lib.require(hidden.stride(1) == 1 and weight.is_contiguous(), "rows must be contiguous")
+    """hidden bf16 ``[n, hidden]``, weight bf16 ``[vocab, hidden]`` (row-major or a
+    :class:`~.gemm.PackedWeight`) -> (int64 ``[n]`` greedy ids, bf16 ``[n, vocab]`` logits when
+    ``return_logits`` else None)."""
+    packed = isinstance(weight, PackedWeight)
+    wt = weight.data if packed else weight
+    device = _lib.require_gpu(hidden, wt, name="lm_head_argmax")
+    _lib.require(hidden.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16, "bf16 operands required")
+    _lib.require(hidden.dim() == 2 and len(weight.shape) == 2 and hidden.shape[1] == weight.shape[1], "shape mismatch")
+    _lib.require(hidden.stride(1) == 1 and wt.is_contiguous(), "rows must be contiguous")
     n, k = hidden.shape
     vocab = weight.shape[0]
     if predicted is None:
@@ -40,13 +44,14 @@ def lm_head_argmax(
     for start in range(0, n, MAX_ROWS):
         rows = min(MAX_ROWS, n - start)
         _lib.call(
-            "oxr_lm_head_argmax", hidden[start:].data_ptr(), rows, weight.data_ptr(), k, vocab,
+            "oxr_lm_head_argmax_packed" if packed else "oxr_lm_head_argmax", hidden[start:].data_ptr(), rows,
+            wt.data_ptr(), k, vocab,
             logits[start:].data_ptr() if logits is not None else None, predicted[start:].data_ptr(),
             workspace.data_ptr(), workspace.numel(), _lib.stream(device),
         )
     return predicted, logits
 
 
-def logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+def logits(hidden: torch.Tensor, weight: Weight) -> torch.Tensor:
     """``LanguageModel.logits``: bf16 ``hidden @ weight.T`` (language.py:213-214)."""
     return lm_head_argmax(hidden, weight, return_logits=True)[1]

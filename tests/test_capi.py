@@ -74,3 +74,10 @@ def test_entry_points_reject_bad_arguments_before_launch() -> None:
                                       None, None, None, None) == -2  # head_dim != 128
     assert lib.oxr_ngram_propose(None, 0, None, None, 1, 9, 3, None, None, None, None) == -2  # max_n > 8
     assert lib.oxr_ngram_propose(None, 0, None, None, 0, 4, 3, None, None, None, None) == 0  # empty batch
+    assert lib.oxr_packed_weight_elems(40, 256) == 48 * 256  # last tile zero-padded
+    assert lib.oxr_packed_weight_elems(0, 256) == 0
+    assert lib.oxr_pack_weight_bf16(16, 32, 100, 4096, None) == -2  # k not a multiple of 128
+    assert lib.oxr_pack_weight_bf16(None, 32, 128, 4096, None) == -1  # no source
+    assert lib.oxr_pack_weight_bf16(4096, 32, 128, 4096 + 64, None) == -1  # overlapping buffers
+    # packed SiLU*mul needs the up rows to start a tile (n % 16 == 0)
+    assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 40, 1, 4096, 40, None) == -2

@@ -97,6 +97,78 @@ def test_linear_add_residual() -> None:
     assert np.mean(got == want) > 0.98
 
 
+@pytest.mark.parametrize("rows,k", [(4096, 2048), (40, 256), (1000, 128)])
+def test_pack_weight_round_trip(rows: int, k: int) -> None:
+    """The packed layout is a pure re-ordering (zero-padded last tile): unpacking gives the
+    weight back bit for bit, and block i of (tile t, step q) holds w[16t + r][128q + 32i + 8g, +8)
+    at lane 16g + r."""
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    w = _rand(g, rows, k)
+    announce("pack", rows, k)
+    p = gemm.pack_weight(w)
+    torch.cuda.synchronize()
+    assert p.data.numel() == -(-rows // 16) * 16 * k
+    assert torch.equal(p.unpack().view(torch.int16), w.view(torch.int16))
+    flat = p.data.view(torch.int16).cpu().numpy()
+    wb = w.view(torch.int16).cpu().numpy()
+    t, q, i, lane = rows // 16 - 1, k // 128 - 1, 2, 37
+    r, gg = lane % 16, lane // 16
+    off = (((t * (k // 128) + q) * 4 + i) * 64 + lane) * 8
+    assert np.array_equal(flat[off:off + 8], wb[16 * t + r, 128 * q + 32 * i + 8 * gg:][:8])
+    tiles = -(-rows // 16)
+    full = flat.reshape(tiles, k // 128, 4, 4, 16, 8).transpose(0, 4, 1, 2, 3, 5).reshape(tiles * 16, k)
+    assert not full[rows:].any()  # the last tile's padding rows are zero
+
+
+@pytest.mark.parametrize("m,k,n,epi", [(32, 2048, 4096, "store"), (32, 2048, 6144, "silu"), (32, 2048, 2048, "partial"),
+                                       (32, 6144, 2048, "partial"), (32, 6144, 2048, "add"), (7, 256, 40, "store"),
+                                       (64, 512, 96, "silu"), (17, 128, 40, "partial")])
+def test_packed_weight_gemm_bit_identical(m: int, k: int, n: int, epi: str) -> None:
+    """Packed and row-major weights run the same arithmetic in the same order."""
+    g = torch.Generator(device="cuda").manual_seed(m + k + n)
+    x = _rand(g, m, k)
+    w = _rand(g, 2 * n if epi == "silu" else n, k, std=0.02)
+    p = gemm.pack_weight(w)
+    announce("packed gemm", m, k, n, epi)
+    if epi == "partial":
+        splits = gemm.partial_splits(n, k)
+        a = torch.full((splits, m, n), float("nan"), device="cuda")
+        b = torch.full((splits, m, n), float("nan"), device="cuda")
+        gemm.linear_partial(x, w, a)
+        gemm.linear_partial(x, p, b)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+        return
+    if epi == "add":
+        r = _rand(g, m, n)
+        a, b = r.clone(), r.clone()
+        gemm.linear_add_(a, x, w)
+        gemm.linear_add_(b, x, p)
+    else:
+        fn = gemm.linear if epi == "store" else gemm.linear_silu_mul
+        a, b = fn(x, w), fn(x, p)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,vocab,k", [(32, 151_936, 2048), (8, 4096 + 40, 2048), (40, 1000, 512), (3, 72, 384)])
+def test_packed_lm_head_bit_identical(m: int, vocab: int, k: int) -> None:
+    """Packed LM head (persistent kernel for m <= 32 and hidden 512/1024/2048, tile kernel otherwise):
+    the same ids and bf16 logits as the row-major weight, including a vocab that is not a multiple
+    of 16 (the padded rows of the last tile never win)."""
+    g = torch.Generator(device="cuda").manual_seed(vocab)
+    hidden, weight = _rand(g, m, k), _rand(g, vocab, k, std=0.02)
+    weight[vocab - 1] = (hidden[0].float() * 0.05).to(torch.bfloat16)  # row 0's max in the last, partial tile
+    p = gemm.pack_weight(weight)
+    announce("packed lm head", m, vocab, k)
+    ia, la = lm_head.lm_head_argmax(hidden, weight, return_logits=True)
+    ib, lb = lm_head.lm_head_argmax(hidden, p, return_logits=True)
+    torch.cuda.synchronize()
+    assert int(ib[0]) == vocab - 1
+    assert torch.equal(ia, ib)
+    assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
+
+
 def test_lm_head_config4_logits_and_argmax() -> None:
     g = torch.Generator(device="cuda").manual_seed(40)
     hidden, weight = _rand(g, 256, 2048), _rand(g, 151_936, 2048, std=0.02)
