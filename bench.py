@@ -38,6 +38,7 @@ language = importlib.import_module(f"{PKG}.language")
 kv_cache = importlib.import_module(f"{PKG}.kv_cache")
 decode_graph = importlib.import_module(f"{PKG}.decode_graph")
 attention = importlib.import_module(f"{PKG}.attention")
+gemm = importlib.import_module(f"{PKG}.gemm")
 workloads = importlib.import_module(f"{PKG}.workloads")
 
 METRIC = "accepted tokens/sec + verify-step latency (us) at B=8,k=3; % HBM roofline"
@@ -101,7 +102,7 @@ def time_attention(config, model, cache, loop, iters: int = 56) -> dict:
     bs = cache.block_size
     table = loop.block_table.to(torch.int64)
     slots = (table.gather(1, (pos.view(b, s) // bs)) * bs + pos.view(b, s) % bs).reshape(-1)
-    out = torch.empty(b, s, c.num_heads, c.head_dim, dtype=torch.bfloat16, device="cuda")
+    out = gemm.packed_rows(b * s, c.num_heads * c.head_dim, "cuda")  # as the step writes it: o_proj's packed x
     max_seq_len = loop.block_table.shape[1] * bs
     ws = torch.zeros(attention.workspace_bytes(b, c.num_kv_heads, max_seq_len), dtype=torch.uint8, device="cuda")
 

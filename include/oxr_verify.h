@@ -134,10 +134,14 @@ int oxr_qk_norm_rope_store_at(const oxr_bf16* qkv, const oxr_bf16* q_weight, con
  * RMSNorm of rows (language.py:69-72): out = bf16(w * bf16(x * 1/sqrt(mean(x^2) + eps))),
  * fp32 statistics.  x bf16 [rows, ldx]; hidden a multiple of 512 up to 4096.
  * Used for the decoder norms after the residual add has been fused into the
- * preceding GEMM (OXR_EPI_ADD_RESIDUAL).
+ * preceding GEMM (OXR_EPI_ADD_RESIDUAL).  out is [rows, ldo], or, with
+ * out_packed != 0, in the packed layout of (4c) (16-row tiles, row length
+ * hidden, room for the rows rounded up to 16; ldo unused) -- the X operand of
+ * oxr_gemm_bf16_packed with OXR_GEMM_X_PACKED.  The same holds for the two
+ * norms below.
  */
 int oxr_rms_norm(const oxr_bf16* x, int64_t ldx, int64_t rows, int64_t hidden, const oxr_bf16* weight, float eps,
-                 oxr_bf16* out, int64_t ldo, oxr_stream_t stream);
+                 oxr_bf16* out, int64_t ldo, int32_t out_packed, oxr_stream_t stream);
 
 /*
  * Embedding gather + first RMSNorm of the verify forward: residual[i] =
@@ -146,7 +150,8 @@ int oxr_rms_norm(const oxr_bf16* x, int64_t ldx, int64_t rows, int64_t hidden, c
  * outside [0, vocab) are clamped.  residual and out are bf16 [rows, hidden].
  */
 int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, int64_t vocab, int64_t hidden,
-                       const oxr_bf16* weight, float eps, oxr_bf16* residual, oxr_bf16* out, oxr_stream_t stream);
+                       const oxr_bf16* weight, float eps, oxr_bf16* residual, oxr_bf16* out, int32_t out_packed,
+                       oxr_stream_t stream);
 
 /*
  * Residual add + RMSNorm from GEMM partials (_add_rms_norm, language.py:94-99):
@@ -156,7 +161,7 @@ int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, 
  */
 int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t rows, int64_t hidden,
                               oxr_bf16* residual, const oxr_bf16* weight, float eps, oxr_bf16* out,
-                              oxr_stream_t stream);
+                              int32_t out_packed, oxr_stream_t stream);
 
 /*
  * (3) Multi-query causal paged attention of the verify step.
@@ -205,7 +210,8 @@ int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight,
                                   const int32_t* block_table, int64_t table_stride, int32_t batch,
                                   int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                   int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale,
-                                  oxr_bf16* out, void* workspace, size_t workspace_bytes, oxr_stream_t stream);
+                                  oxr_bf16* out, int32_t out_packed, void* workspace, size_t workspace_bytes,
+                                  oxr_stream_t stream);
 
 /*
  * (4a) Weight-streaming bf16 GEMM Y = X * W^T with a fused epilogue.
@@ -255,7 +261,7 @@ int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight
                        oxr_stream_t stream);
 
 /*
- * (4c) Packed weights.  The reference keeps nn.Linear weights row-major
+ * (4c) Packed weights and token rows.  The reference keeps nn.Linear weights row-major
  * ([rows, k], language.py:234-245 and the LM head of :213-214); these entry
  * points take the same weights re-ordered once, at load time, into the order
  * the GEMM kernels consume them: for each 16-row tile t and 128-column step q,
@@ -269,10 +275,21 @@ int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight
  */
 size_t oxr_packed_weight_elems(int64_t rows, int64_t k);
 int oxr_pack_weight_bf16(const oxr_bf16* w, int64_t rows, int64_t k, oxr_bf16* packed, oxr_stream_t stream);
+/*
+ * Token rows may travel between kernels in the same layout (16-token tiles,
+ * row length k, rows past m padding): flags OXR_GEMM_X_PACKED (x packed; ldx
+ * unused) and OXR_GEMM_Y_PACKED (y packed with row length n, a multiple of
+ * 128; ldy unused; OXR_EPI_STORE and OXR_EPI_SILU_MUL).  Producers of packed
+ * rows: the norms' out_packed, oxr_qk_norm_rope_paged_extend's out_packed
+ * and OXR_GEMM_Y_PACKED.  A packed [m, k] buffer holds ceil(m / 16) * 16 * k
+ * elements.
+ */
+#define OXR_GEMM_X_PACKED 1
+#define OXR_GEMM_Y_PACKED 2
 int oxr_gemm_bf16_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed, int64_t k, int64_t n,
-                         int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream);
+                         int32_t epilogue, oxr_bf16* y, int64_t ldy, int32_t flags, oxr_stream_t stream);
 int oxr_gemm_bf16_partial_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed, int64_t k,
-                                 int64_t n, float* partials, int32_t k_splits, oxr_stream_t stream);
+                                 int64_t n, float* partials, int32_t k_splits, int32_t flags, oxr_stream_t stream);
 int oxr_lm_head_argmax_packed(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight_packed, int64_t hidden_size,
                               int64_t vocab, oxr_bf16* logits, int64_t* predicted, void* workspace,
                               size_t workspace_bytes, oxr_stream_t stream);

@@ -40,15 +40,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_qk_norm_rope_paged_extend": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _F32, _P, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32,
-         _I64, _I32, _F32, _P, _P, _SZ, _P],
+         _I64, _I32, _F32, _P, _I32, _P, _SZ, _P],
     ),
     "oxr_qk_norm_rope_store_at": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _F32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
     ),
-    "oxr_rms_norm": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _F32, _P, _I64, _P]),
-    "oxr_embed_rms_norm": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _F32, _P, _P, _P]),
-    "oxr_add_partials_rms_norm": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _F32, _P, _P]),
+    "oxr_rms_norm": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _F32, _P, _I64, _I32, _P]),
+    "oxr_embed_rms_norm": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _F32, _P, _P, _I32, _P]),
+    "oxr_add_partials_rms_norm": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _F32, _P, _I32, _P]),
     "oxr_gemm_bf16": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I64, _P]),
     "oxr_gemm_bf16_partial_splits": (ctypes.c_int32, [_I64, _I64]),
     "oxr_gemm_bf16_partial": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P]),
@@ -56,8 +56,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_lm_head_argmax": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "oxr_packed_weight_elems": (ctypes.c_size_t, [_I64, _I64]),
     "oxr_pack_weight_bf16": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
-    "oxr_gemm_bf16_packed": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I64, _P]),
-    "oxr_gemm_bf16_partial_packed": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P]),
+    "oxr_gemm_bf16_packed": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I64, _I32, _P]),
+    "oxr_gemm_bf16_partial_packed": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I32, _P]),
     "oxr_lm_head_argmax_packed": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "oxr_qk_norm_rope_store": (
         ctypes.c_int,

@@ -11,6 +11,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .gemm import PackedMatrix
 
 
 def workspace_bytes(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
@@ -64,14 +65,15 @@ def qk_norm_rope_paged_extend(
     qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, cos_table: torch.Tensor,
     sin_table: torch.Tensor, positions: torch.Tensor, eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
     slots: torch.Tensor, seq_lens: torch.Tensor, block_table: torch.Tensor, num_heads: int, *,
-    scale: float | None = None, max_seq_len: int | None = None, out: torch.Tensor | None = None,
+    scale: float | None = None, max_seq_len: int | None = None, out: torch.Tensor | PackedMatrix | None = None,
     workspace: torch.Tensor | None = None,
-) -> torch.Tensor:
+) -> torch.Tensor | PackedMatrix:
     """The decoder layer's attention block of the verify step (oxr_runtime/language.py:311-316) in one
     launch: ``kernels.qk_norm_rope_store`` (q/k RMSNorm + RoPE at ``positions``, K/V into the cache at
     ``slots``) followed by :func:`paged_extend`, with q kept on chip.  ``qkv`` is ``[B*S, (H+2KV)*D]``
-    for the S new tokens of each of the B sequences; returns ``[B, S, H, D]`` and leaves the cache
-    rows exactly as the two separate calls would."""
+    for the S new tokens of each of the B sequences; returns ``[B, S, H, D]`` (or fills ``out``
+    given as a packed ``[B*S, H*D]`` :class:`~.gemm.PackedMatrix`, the o_proj GEMM's x) and leaves
+    the cache rows exactly as the two separate calls would."""
     device = _lib.require_gpu(qkv, q_weight, k_weight, cos_table, sin_table, positions, k_cache, v_cache, slots,
                               seq_lens, block_table, name="qk_norm_rope_paged_extend")
     _lib.require(qkv.dtype == torch.bfloat16 and qkv.dim() == 2 and qkv.is_contiguous(), "qkv must be contiguous bf16")
@@ -94,6 +96,13 @@ def qk_norm_rope_paged_extend(
         scale = d ** -0.5
     if out is None:
         out = torch.empty(b, s, num_heads, d, dtype=torch.bfloat16, device=device)
+    packed = isinstance(out, PackedMatrix)
+    if packed:
+        _lib.require(out.shape == (n, num_heads * d) and out.data.numel() >= -(-n // 16) * 16 * num_heads * d,
+                     "qk_norm_rope_paged_extend: packed out must be [B*S, H*D]")
+    else:
+        _lib.require(out.shape == (b, s, num_heads, d) and out.is_contiguous(), "out must be contiguous [B, S, H, D]")
+    out_t = out.data if packed else out
     need = workspace_bytes(b, kv, max_seq_len)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
@@ -102,7 +111,7 @@ def qk_norm_rope_paged_extend(
         cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0], positions.data_ptr(), float(eps),
         k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), num_blocks * block_size, seq_lens.data_ptr(),
         block_table.data_ptr(), block_table.stride(0), b, s, num_heads, kv, d, block_size, num_blocks, max_seq_len,
-        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-        _lib.stream(device),
+        float(scale), out_t.data_ptr(), 1 if packed else 0, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _lib.stream(device),
     )
     return out

@@ -77,6 +77,15 @@ __device__ __forceinline__ u32x4 ld128_nt(const void* p) {
 }
 __device__ __forceinline__ void st128(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// Element (row, k) of a [rows, K] bf16 matrix in the packed layout the GEMMs
+// stream (weights, and token rows between kernels): 16-row tiles; per tile and
+// 128-column step four contiguous 1 KiB blocks, block i holding, for lane
+// 16g + r, row r's columns [32i + 8g, +8).  K is a multiple of 128.
+__device__ __forceinline__ int64_t packed_offset(int64_t row, int64_t k, int64_t K) {
+  return ((((row >> 4) * (K >> 7) + (k >> 7)) * 4 + ((k >> 5) & 3)) * 64 + ((k >> 3) & 3) * 16 + (row & 15)) * 8 +
+         (k & 7);
+}
+
 }  // namespace oxr
 
 // Host-side helpers shared by the entry points.

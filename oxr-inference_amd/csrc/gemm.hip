@@ -21,7 +21,10 @@
 //   four contiguous 1 KiB blocks, block i holding the fragments of k-step i in
 //   lane order (lane 16g + r: W[16t + r][128q + 32i + 8g, +8)), so each load
 //   instruction reads 1 KiB of contiguous memory.  Same arithmetic, same
-//   order: packed and row-major results are bit-identical.
+//   order: packed and row-major results are bit-identical.  The token rows X
+//   may come packed the same way (PX: 16-token tiles, written so by the
+//   kernels that produce them), and kStore / kSiluMul can write Y packed for
+//   the next GEMM.
 // * The waves' fp32 tiles are summed in LDS in a fixed order, then the
 //   epilogue runs on the finished tile:
 //     kStore        Y = bf16(acc)
@@ -77,6 +80,7 @@ struct GemmArgs {
   int64_t N;        // output columns (weight rows; gate rows for kSiluMul)
   bf16_t* y;        // kStore / kSiluMul: [M, ldy]; kArgmax: optional logits [M, ldy]; kAddResidual: R [M, ldy]
   int64_t ldy;
+  int y_packed;     // kStore / kSiluMul: y in the packed layout with row length N (ldy unused)
   uint64_t* best;   // kArgmax: [num_tiles, M]
   float* part;      // kPartial: [k_splits, M, N]
 };
@@ -87,7 +91,7 @@ struct Stage {
   u32x4 x[NB][4];
 };
 
-template <int NA, int NB, int EPI, int WAVES, bool PW>
+template <int NA, int NB, int EPI, int WAVES, bool PW, bool PX>
 __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
   constexpr int kTileRows = 16 * NA;                          // output columns of this workgroup
   constexpr int kLoadTiles = (EPI == kSiluMul) ? 2 * NA : NA;  // gate + up tiles for kSiluMul
@@ -112,12 +116,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
     if (EPI == kSiluMul && a >= NA) row += args.N;
     wrow[a] = PW ? args.w + (row >> 4) * (K * 16) + lane * 8 : args.w + row * K + 8 * g;
   }
-  // Token rows past M read row 0 and multiply into accumulators nobody stores.
+  // Token rows past M read row 0 (packed: the tile's padding) and multiply
+  // into accumulators nobody stores.
   const bf16_t* xrow[NB];
 #pragma unroll
   for (int bt = 0; bt < NB; ++bt) {
     const int tok = 16 * bt + r;
-    xrow[bt] = args.x + (int64_t)(tok < args.M ? tok : 0) * args.ldx + 8 * g;
+    xrow[bt] = PX ? args.x + (int64_t)bt * (K * 16) + lane * 8
+                  : args.x + (int64_t)(tok < args.M ? tok : 0) * args.ldx + 8 * g;
   }
 
   f32x4 acc[kLoadTiles][NB];
@@ -134,7 +140,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st.x[bt][i] = ld128(xrow[bt] + k + 32 * i);
+      for (int i = 0; i < 4; ++i) st.x[bt][i] = ld128(PX ? xrow[bt] + 16 * k + 512 * i : xrow[bt] + k + 32 * i);
   };
 
   auto compute = [&](const Stage<kLoadTiles, NB>& st) {
@@ -265,7 +271,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
             out[j] = v;
           }
         }
-        bf16_t* dst = args.y + (int64_t)tok * args.ldy + col0;
+        bf16_t* dst = args.y + (args.y_packed ? packed_offset(tok, col0, args.N) : (int64_t)tok * args.ldy + col0);
         if constexpr (EPI == kAddResidual) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
@@ -498,43 +504,50 @@ struct LaunchConfig {
   int k_splits;  // k slices across workgroups (kPartial only)
 };
 
-template <int NA, int NB, int EPI, int WAVES, bool PW>
+template <int NA, int NB, int EPI, int WAVES, bool PW, bool PX>
 int launch_gemm(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   const int64_t tiles = (a.N + 16 * NA - 1) / (16 * NA);
-  hipLaunchKernelGGL((gemm_kernel<NA, NB, EPI, WAVES, PW>), dim3((unsigned)tiles, (unsigned)c.k_splits),
+  hipLaunchKernelGGL((gemm_kernel<NA, NB, EPI, WAVES, PW, PX>), dim3((unsigned)tiles, (unsigned)c.k_splits),
                      dim3(64 * WAVES), 0, s, a);
   return OXR_LAUNCH_STATUS();
 }
 
-template <int NA, int EPI, int WAVES, bool PW>
+template <int NA, int EPI, int WAVES, bool PW, bool PX>
 int dispatch_nb(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   switch ((a.M + 15) / 16) {
-    case 1: return launch_gemm<NA, 1, EPI, WAVES, PW>(a, c, s);
-    case 2: return launch_gemm<NA, 2, EPI, WAVES, PW>(a, c, s);
-    case 3: return launch_gemm<NA, 3, EPI, WAVES, PW>(a, c, s);
-    case 4: return launch_gemm<NA, 4, EPI, WAVES, PW>(a, c, s);
+    case 1: return launch_gemm<NA, 1, EPI, WAVES, PW, PX>(a, c, s);
+    case 2: return launch_gemm<NA, 2, EPI, WAVES, PW, PX>(a, c, s);
+    case 3: return launch_gemm<NA, 3, EPI, WAVES, PW, PX>(a, c, s);
+    case 4: return launch_gemm<NA, 4, EPI, WAVES, PW, PX>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
-template <int NA, int EPI, bool PW>
+template <int NA, int EPI, bool PW, bool PX>
 int dispatch_waves(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
   switch (c.waves) {
-    case 1: return dispatch_nb<NA, EPI, 1, PW>(a, c, s);
-    case 2: return dispatch_nb<NA, EPI, 2, PW>(a, c, s);
-    case 4: return dispatch_nb<NA, EPI, 4, PW>(a, c, s);
-    case 8: return dispatch_nb<NA, EPI, 8, PW>(a, c, s);
+    case 1: return dispatch_nb<NA, EPI, 1, PW, PX>(a, c, s);
+    case 2: return dispatch_nb<NA, EPI, 2, PW, PX>(a, c, s);
+    case 4: return dispatch_nb<NA, EPI, 4, PW, PX>(a, c, s);
+    case 8: return dispatch_nb<NA, EPI, 8, PW, PX>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
 
+// Operand layouts: row-major weight and X; packed weight, row-major X; both
+// packed (the verify forward's own path; the LM head stages X itself).
+enum Layout { kRowMajor = 0, kPackedW = 1, kPackedWX = 2 };
+
 template <int EPI>
-int dispatch(const GemmArgs& a, const LaunchConfig& c, bool packed, hipStream_t s) {
-  switch (c.na * 2 + (packed ? 1 : 0)) {
-    case 2: return dispatch_waves<1, EPI, false>(a, c, s);
-    case 3: return dispatch_waves<1, EPI, true>(a, c, s);
-    case 4: return dispatch_waves<2, EPI, false>(a, c, s);
-    case 5: return dispatch_waves<2, EPI, true>(a, c, s);
+int dispatch(const GemmArgs& a, const LaunchConfig& c, Layout layout, hipStream_t s) {
+  if (EPI == kArgmax && layout == kPackedWX) return OXR_ERR_UNSUPPORTED;
+  switch (c.na * 4 + (int)layout) {
+    case 4: return dispatch_waves<1, EPI, false, false>(a, c, s);
+    case 5: return dispatch_waves<1, EPI, true, false>(a, c, s);
+    case 6: return dispatch_waves<1, EPI, true, EPI != kArgmax>(a, c, s);
+    case 8: return dispatch_waves<2, EPI, false, false>(a, c, s);
+    case 9: return dispatch_waves<2, EPI, true, false>(a, c, s);
+    case 10: return dispatch_waves<2, EPI, true, EPI != kArgmax>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
@@ -586,32 +599,44 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const bf16_t* __restri
   }
 }
 
+// flags: OXR_GEMM_X_PACKED (x packed; ldx unused), OXR_GEMM_Y_PACKED (y packed
+// with row length n; ldy unused; kStore / kSiluMul).  Row-major weights take
+// neither.
 int gemm_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n, int32_t epilogue,
-               oxr_bf16* y, int64_t ldy, bool packed, oxr_stream_t stream) {
+               oxr_bf16* y, int64_t ldy, bool packed, int32_t flags, oxr_stream_t stream) {
+  const bool xp = flags & OXR_GEMM_X_PACKED, yp = flags & OXR_GEMM_Y_PACKED;
+  OXR_RETURN_IF((flags & ~(OXR_GEMM_X_PACKED | OXR_GEMM_Y_PACKED)) != 0 || (!packed && flags != 0), OXR_ERR_INVALID_ARG);
+  if (xp) ldx = k;
+  if (yp) ldy = n;
   int st = check_common(x, ldx, m, w, k, n);
   if (st) return st;
   OXR_RETURN_IF(epilogue != kStore && epilogue != kSiluMul && epilogue != kAddResidual, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(!y || ldy < n || ldy % 4 != 0 || (uintptr_t)y % 8 != 0, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(packed && epilogue == kSiluMul && n % 16 != 0, OXR_ERR_UNSUPPORTED);  // up rows start a tile
+  OXR_RETURN_IF(yp && (epilogue == kAddResidual || n % kKStep != 0), OXR_ERR_UNSUPPORTED);
   if (m == 0) return OXR_OK;
-  GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, nullptr, nullptr};
+  GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, yp ? 1 : 0, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
   const LaunchConfig c = choose_config(n, k, false);
-  if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, packed, s);
-  if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, packed, s);
-  return dispatch<kStore>(a, c, packed, s);
+  const Layout layout = !packed ? kRowMajor : (xp ? kPackedWX : kPackedW);
+  if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, layout, s);
+  if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, layout, s);
+  return dispatch<kStore>(a, c, layout, s);
 }
 
 int gemm_partial_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
-                       float* partials, int32_t k_splits, bool packed, oxr_stream_t stream) {
+                       float* partials, int32_t k_splits, bool packed, int32_t flags, oxr_stream_t stream) {
+  OXR_RETURN_IF((flags & ~OXR_GEMM_X_PACKED) != 0 || (!packed && flags != 0), OXR_ERR_INVALID_ARG);
+  const bool xp = flags & OXR_GEMM_X_PACKED;
+  if (xp) ldx = k;
   int st = check_common(x, ldx, m, w, k, n);
   if (st) return st;
   OXR_RETURN_IF(!partials || (uintptr_t)partials % 16 != 0 || n % 4 != 0, OXR_ERR_INVALID_ARG);
   const LaunchConfig c = choose_config(n, k, true);
   OXR_RETURN_IF(k_splits != c.k_splits, OXR_ERR_INVALID_ARG);
   if (m == 0) return OXR_OK;
-  GemmArgs a{x, ldx, (int)m, w, k, n, nullptr, 0, nullptr, partials};
-  return dispatch<kPartial>(a, c, packed, (hipStream_t)stream);
+  GemmArgs a{x, ldx, (int)m, w, k, n, nullptr, 0, 0, nullptr, partials};
+  return dispatch<kPartial>(a, c, !packed ? kRowMajor : (xp ? kPackedWX : kPackedW), (hipStream_t)stream);
 }
 
 int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
@@ -641,10 +666,10 @@ int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int
                     : launch_lm_head_lds_k<2, true>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits,
                                                     best, num_best, s);
   } else {
-    GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, best, nullptr};
+    GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, 0, best, nullptr};
     const LaunchConfig c = choose_config(vocab, hidden_size, false);
     num_best = (int)((vocab + 16 * c.na - 1) / (16 * c.na));
-    st = dispatch<kArgmax>(a, c, packed, s);
+    st = dispatch<kArgmax>(a, c, packed ? kPackedW : kRowMajor, s);
   }
   if (st) return st;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(best),
@@ -677,12 +702,13 @@ extern "C" int oxr_pack_weight_bf16(const oxr_bf16* w, int64_t rows, int64_t k, 
 
 extern "C" int oxr_gemm_bf16(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
                              int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream) {
-  return oxr::gemm_entry(x, ldx, m, w, k, n, epilogue, y, ldy, false, stream);
+  return oxr::gemm_entry(x, ldx, m, w, k, n, epilogue, y, ldy, false, 0, stream);
 }
 
 extern "C" int oxr_gemm_bf16_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed, int64_t k,
-                                    int64_t n, int32_t epilogue, oxr_bf16* y, int64_t ldy, oxr_stream_t stream) {
-  return oxr::gemm_entry(x, ldx, m, w_packed, k, n, epilogue, y, ldy, true, stream);
+                                    int64_t n, int32_t epilogue, oxr_bf16* y, int64_t ldy, int32_t flags,
+                                    oxr_stream_t stream) {
+  return oxr::gemm_entry(x, ldx, m, w_packed, k, n, epilogue, y, ldy, true, flags, stream);
 }
 
 extern "C" int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k) {
@@ -691,13 +717,13 @@ extern "C" int32_t oxr_gemm_bf16_partial_splits(int64_t n, int64_t k) {
 
 extern "C" int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k,
                                      int64_t n, float* partials, int32_t k_splits, oxr_stream_t stream) {
-  return oxr::gemm_partial_entry(x, ldx, m, w, k, n, partials, k_splits, false, stream);
+  return oxr::gemm_partial_entry(x, ldx, m, w, k, n, partials, k_splits, false, 0, stream);
 }
 
 extern "C" int oxr_gemm_bf16_partial_packed(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w_packed,
-                                            int64_t k, int64_t n, float* partials, int32_t k_splits,
+                                            int64_t k, int64_t n, float* partials, int32_t k_splits, int32_t flags,
                                             oxr_stream_t stream) {
-  return oxr::gemm_partial_entry(x, ldx, m, w_packed, k, n, partials, k_splits, true, stream);
+  return oxr::gemm_partial_entry(x, ldx, m, w_packed, k, n, partials, k_splits, true, flags, stream);
 }
 
 extern "C" size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab) {

@@ -35,7 +35,7 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(const bf16_t* __r
                                                                const float* __restrict__ partials, int k_splits,
                                                                int rows, int D, const bf16_t* __restrict__ w, float eps,
                                                                bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
-                                                               int64_t ldo) {
+                                                               int64_t ldo, int out_packed) {
   __shared__ float wave_ss[kMaxThreads / kWave];
   const int row = blockIdx.x;
   const int col = threadIdx.x * 8;
@@ -91,23 +91,24 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(const bf16_t* __r
     const float y1 = hi_bf(wd[e]) * round_bf16(hi_bf(xd[e]) * r);
     o[e] = pack_bf(y0, y1);
   }
-  st128(out + (int64_t)row * ldo + col, u32x4{o[0], o[1], o[2], o[3]});
+  st128(out + (out_packed ? packed_offset(row, col, D) : (int64_t)row * ldo + col), u32x4{o[0], o[1], o[2], o[3]});
   if constexpr (MODE != kRows) st128(residual + (int64_t)row * ldo + col, v);
 }
 
 template <int MODE>
 int launch(const bf16_t* x, int64_t ldx, const int64_t* ids, int64_t vocab, const float* partials, int k_splits,
-           int rows, int D, const bf16_t* w, float eps, bf16_t* residual, bf16_t* out, int64_t ldo, hipStream_t s) {
+           int rows, int D, const bf16_t* w, float eps, bf16_t* residual, bf16_t* out, int64_t ldo, int out_packed,
+           hipStream_t s) {
   const dim3 grid(rows), block(D / 8);
   if (MODE == kAddPartials && k_splits == 2)
     hipLaunchKernelGGL((rms_norm_kernel<MODE, 2>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
-                       w, eps, residual, out, ldo);
+                       w, eps, residual, out, ldo, out_packed);
   else if (MODE == kAddPartials && k_splits == 4)
     hipLaunchKernelGGL((rms_norm_kernel<MODE, 4>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
-                       w, eps, residual, out, ldo);
+                       w, eps, residual, out, ldo, out_packed);
   else
     hipLaunchKernelGGL((rms_norm_kernel<MODE, 0>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
-                       w, eps, residual, out, ldo);
+                       w, eps, residual, out, ldo, out_packed);
   return OXR_LAUNCH_STATUS();
 }
 
@@ -122,31 +123,31 @@ int check(int64_t rows, int64_t D, int64_t ld, int64_t ldo) {
 }  // namespace oxr
 
 extern "C" int oxr_rms_norm(const oxr_bf16* x, int64_t ldx, int64_t rows, int64_t hidden, const oxr_bf16* weight,
-                            float eps, oxr_bf16* out, int64_t ldo, oxr_stream_t stream) {
+                            float eps, oxr_bf16* out, int64_t ldo, int32_t out_packed, oxr_stream_t stream) {
   using namespace oxr;
-  int st = check(rows, hidden, ldx, ldo);
+  int st = check(rows, hidden, ldx, out_packed ? hidden : ldo);
   if (st) return st;
   if (rows == 0) return OXR_OK;
   OXR_RETURN_IF(!x || !weight || !out, OXR_ERR_INVALID_ARG);
   return launch<kRows>(x, ldx, nullptr, 0, nullptr, 0, (int)rows, (int)hidden, weight, eps, nullptr, out, ldo,
-                       (hipStream_t)stream);
+                       out_packed ? 1 : 0, (hipStream_t)stream);
 }
 
 extern "C" int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, int64_t vocab,
                                   int64_t hidden, const oxr_bf16* weight, float eps, oxr_bf16* residual,
-                                  oxr_bf16* out, oxr_stream_t stream) {
+                                  oxr_bf16* out, int32_t out_packed, oxr_stream_t stream) {
   using namespace oxr;
   int st = check(rows, hidden, hidden, hidden);
   if (st) return st;
   if (rows == 0) return OXR_OK;
   OXR_RETURN_IF(!ids || !table || vocab <= 0 || !weight || !residual || !out, OXR_ERR_INVALID_ARG);
   return launch<kEmbed>(table, hidden, ids, vocab, nullptr, 0, (int)rows, (int)hidden, weight, eps, residual, out,
-                        hidden, (hipStream_t)stream);
+                        hidden, out_packed ? 1 : 0, (hipStream_t)stream);
 }
 
 extern "C" int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t rows, int64_t hidden,
                                          oxr_bf16* residual, const oxr_bf16* weight, float eps, oxr_bf16* out,
-                                         oxr_stream_t stream) {
+                                         int32_t out_packed, oxr_stream_t stream) {
   using namespace oxr;
   int st = check(rows, hidden, hidden, hidden);
   if (st) return st;
@@ -154,5 +155,5 @@ extern "C" int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits
   if (rows == 0) return OXR_OK;
   OXR_RETURN_IF(!partials || !residual || !weight || !out, OXR_ERR_INVALID_ARG);
   return launch<kAddPartials>(nullptr, hidden, nullptr, 0, partials, k_splits, (int)rows, (int)hidden, weight, eps,
-                              residual, out, hidden, (hipStream_t)stream);
+                              residual, out, hidden, out_packed ? 1 : 0, (hipStream_t)stream);
 }

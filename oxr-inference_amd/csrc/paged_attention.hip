@@ -21,9 +21,11 @@
 //
 // Per wave, 32 keys at a time (two 16-key MFMA tiles), all in registers:
 //   S^T tile = K[16 keys x 128] * Q^T           4 v_mfma_f32_16x16x32_bf16 / tile
-//     A lane reads 64 contiguous bytes of one key row, which is exactly its
-//     A-operand fragment; Q^T stays in registers.  Lane (r = l % 16, g = l / 16)
-//     gets the scores of keys 4g..4g+3 of the tile for query row r.
+//     MFMA i takes dims [32i, 32i + 32): lane (r = l % 16, g = l / 16) loads
+//     K[key r][32i + 8g, +8), its A-operand fragment, so the 4 lanes of a key
+//     read 64 contiguous bytes per instruction (half the cache lines of a
+//     lane-contiguous mapping); Q^T stays in registers in the same mapping.
+//     Lane (r, g) gets the scores of keys 4g..4g+3 of the tile for query row r.
 //   online softmax per row in the exp2 domain (scale * log2 e folded in)
 //   V^T fragments by MFMA: V[16 keys x 32 dims] times a 0/1 selector gives
 //     C[key][n] = V[key][n] (or [n + 16]) in the C layout, i.e. lane (n, g) holds
@@ -47,7 +49,7 @@ constexpr uint32_t kBf16One = 0x3f80u;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 struct PairRegs {
-  u32x4 k[2][4];  // tile p: K[key 16p + r][32g + 8i .. +7], i = 0..3
+  u32x4 k[2][4];  // tile p: K[key 16p + r][32i + 8g .. +7], i = 0..3
   u32x4 v[2][4];  // tile p: V[key 16p + r][32c + 8g .. +7], c = 0..3
 };
 
@@ -76,10 +78,10 @@ __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict
     const int64_t page = ((p ? blk1 : blk0) << log2_bs) * KV * kD;  // wave-uniform
     const uint32_t tok = (uint32_t)min(t0 + 16 * p + r, L - 1);
     const uint32_t off = ((tok & ((1u << log2_bs) - 1)) * (uint32_t)KV + (uint32_t)kvh) * kD;
-    const bf16_t* ks = k_cache + page + off + 32 * g;
+    const bf16_t* ks = k_cache + page + off + 8 * g;
     const bf16_t* vs = v_cache + page + off + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld128(ks + 8 * i);
+    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld128(ks + 32 * i);
 #pragma unroll
     for (int c = 0; c < 4; ++c) pr.v[p][c] = ld128(vs + 32 * c);
   }
@@ -93,6 +95,12 @@ __device__ __forceinline__ u32x4 selector(int r, int g, int shift) {
   for (int e = 0; e < 8; ++e)
     if (e == jj) w[e >> 1] |= kBf16One << (16 * (e & 1));
   return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Output vector of 4 dims at (token, column) of out [B * S, H * 128]:
+// row-major, or the packed layout of the o_proj GEMM's X operand.
+__device__ __forceinline__ uint32_t* out_vec(bf16_t* out, int64_t tok, int64_t col, int64_t row_len, int packed) {
+  return reinterpret_cast<uint32_t*>(out + (packed ? packed_offset(tok, col, row_len) : tok * row_len + col));
 }
 
 constexpr int kWaves = 8;          // waves per workgroup
@@ -125,7 +133,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const bf16_t* __restrict__ q, const bf16_t* k_cache, const bf16_t* v_cache, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ block_table, int64_t table_stride, int S, int H, int KV, int log2_bs,
     int64_t num_blocks, float scale_log2, int max_seq_len, int splits, float* __restrict__ part_o,
-    float* __restrict__ part_ml, bf16_t* __restrict__ out, RopeArgs ra) {
+    float* __restrict__ part_ml, bf16_t* __restrict__ out, int out_packed, RopeArgs ra) {
   __shared__ float s_o[kWaves][kRows][kD];
   __shared__ u32x4 s_q[kFused ? kRows : 1][kD / 8];
   __shared__ u32x4 s_newk[kFused ? kMaxNew : 1][kD / 8], s_newv[kFused ? kMaxNew : 1][kD / 8];
@@ -249,9 +257,9 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   if (r < R) {
     const int s = r / G, hh = r % G;
     if constexpr (!kFused) {
-      const bf16_t* src = q + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + 32 * g;
+      const bf16_t* src = q + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + 8 * g;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qf[i] = ld128(src + 8 * i);
+      for (int i = 0; i < 4; ++i) qf[i] = ld128(src + 32 * i);
     }
     qpos = L - S + s;
   } else {
@@ -267,7 +275,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   if constexpr (kFused) {
     if (r < R) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qf[i] = s_q[r][4 * g + i];
+      for (int i = 0; i < 4; ++i) qf[i] = s_q[r][4 * i + g];
     }
   }
 
@@ -286,7 +294,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
           const int ns = min(t0 + 16 * p + r, L - 1) - (L - S);  // keys past L re-read row L - 1
           if (ns >= 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) cur.k[p][i] = s_newk[ns][4 * g + i];  // dims 32g + 8i
+            for (int i = 0; i < 4; ++i) cur.k[p][i] = s_newk[ns][4 * i + g];  // dims 32i + 8g
 #pragma unroll
             for (int c = 0; c < 4; ++c) cur.v[p][c] = s_newv[ns][4 * c + g];  // dims 32c + 8g
           }
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     if (single) {
       const float inv = l > 0.f ? 1.0f / l : 0.f;
       const int s = rr / G, hh = rr % G;
-      uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
+      uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh * G + hh) * kD + d0, H * kD, out_packed);
       dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
       dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
     } else {
@@ -417,7 +425,7 @@ __global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(cons
                                                                           const float* __restrict__ part_ml,
                                                                           const int32_t* __restrict__ seq_lens, int S,
                                                                           int H, int KV, int max_seq_len, int splits,
-                                                                          bf16_t* __restrict__ out) {
+                                                                          bf16_t* __restrict__ out, int out_packed) {
   constexpr int kChunk = 8;  // splits whose partials are requested together
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int G = H / KV;
@@ -455,7 +463,7 @@ __global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(cons
   if (L <= span) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int s = rr / G, hh = rr % G;
-  uint32_t* dst = reinterpret_cast<uint32_t*>(out + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + d0);
+  uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh * G + hh) * kD + d0, H * kD, out_packed);
   dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
   dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
 }
@@ -486,8 +494,8 @@ namespace {
 int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache, const int32_t* seq_lens,
                         const int32_t* block_table, int64_t table_stride, int32_t batch, int32_t tokens_per_seq,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                        int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out, void* workspace,
-                        size_t workspace_bytes, const RopeArgs* ra, hipStream_t s) {
+                        int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out, int out_packed,
+                        void* workspace, size_t workspace_bytes, const RopeArgs* ra, hipStream_t s) {
   OXR_RETURN_IF(batch < 0 || tokens_per_seq <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
                     table_stride < 0 || max_seq_len <= 0,
                 OXR_ERR_INVALID_ARG);
@@ -516,17 +524,17 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   if (ra) {
     hipLaunchKernelGGL(paged_extend_kernel<true>, grid, block, 0, s, nullptr, k_cache, v_cache, seq_lens, block_table,
                        table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
-                       max_seq_len, splits, part_o, part_ml, out, *ra);
+                       max_seq_len, splits, part_o, part_ml, out, out_packed, *ra);
   } else {
     hipLaunchKernelGGL(paged_extend_kernel<false>, grid, block, 0, s, q, k_cache, v_cache, seq_lens, block_table,
                        table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
-                       max_seq_len, splits, part_o, part_ml, out, RopeArgs{});
+                       max_seq_len, splits, part_o, part_ml, out, out_packed, RopeArgs{});
   }
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;
   const int rows = tokens_per_seq * (num_heads / num_kv_heads);
   hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(rows * kD / 4), 0, s, part_o, part_ml,
-                     seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, out);
+                     seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, out, out_packed);
   return OXR_LAUNCH_STATUS();
 }
 
@@ -541,7 +549,7 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
                                 oxr_stream_t stream) {
   return oxr::launch_paged_extend(q, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
                                   num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
-                                  workspace, workspace_bytes, nullptr, (hipStream_t)stream);
+                                  0, workspace, workspace_bytes, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
@@ -552,8 +560,8 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
                                              int64_t table_stride, int32_t batch, int32_t tokens_per_seq,
                                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                              int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale,
-                                             oxr_bf16* out, void* workspace, size_t workspace_bytes,
-                                             oxr_stream_t stream) {
+                                             oxr_bf16* out, int32_t out_packed, void* workspace,
+                                             size_t workspace_bytes, oxr_stream_t stream) {
   using namespace oxr;
   OXR_RETURN_IF(num_slots < 0, OXR_ERR_INVALID_ARG);
   // One 16-lane job per q row and per new K and V row: 32 per workgroup.
@@ -567,5 +575,5 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
                     k_cache, v_cache};
   return launch_paged_extend(nullptr, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
                              num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
-                             workspace, workspace_bytes, &ra, (hipStream_t)stream);
+                             out_packed ? 1 : 0, workspace, workspace_bytes, &ra, (hipStream_t)stream);
 }

@@ -11,8 +11,9 @@ These replace the ``nn.Linear`` projections of the reference decoder layer (lang
                         and the next RMSNorm in one pass
 
 Every function takes the weight either row-major (a ``torch.Tensor`` ``[n, k]``, as nn.Linear holds
-it) or as a :class:`PackedWeight` made once by :func:`pack_weight`, which the kernels stream
-markedly faster; the results are bit-identical.
+it) or as a :class:`PackedMatrix` made once by :func:`pack_weight`, which the kernels stream
+markedly faster; the results are bit-identical.  With a packed weight the token rows ``x`` and the
+output may be packed too (the verify forward keeps them so between its kernels).
 """
 
 from __future__ import annotations
@@ -25,19 +26,22 @@ from . import _lib
 
 
 @dataclass(frozen=True)
-class PackedWeight:
-    """A bf16 ``[rows, k]`` weight re-ordered once into the order the GEMM kernels stream it
-    (``oxr_pack_weight_bf16``): per 16-row tile and 128-column step, four contiguous 1 KiB blocks
-    of MFMA fragments, so every load instruction reads contiguous memory.  ``data`` is 1-D (the
-    last tile zero-padded) so it cannot be mistaken for a row-major matrix."""
+class PackedMatrix:
+    """A bf16 ``[rows, cols]`` matrix in the order the GEMM kernels stream their operands
+    (csrc/gemm.hip): per 16-row tile and 128-column step, four contiguous 1 KiB blocks of MFMA
+    fragments, so every load instruction reads contiguous memory.  Weights are packed once by
+    :func:`pack_weight`; token rows travel between the verify forward's kernels in this layout
+    (:func:`packed_rows` allocates them).  ``data`` is 1-D (the last tile padded) so it cannot be
+    mistaken for a row-major matrix; it may hold more rows than ``rows`` (a buffer for up to N
+    rows holds every smaller row count as a prefix)."""
 
     data: torch.Tensor
     rows: int
-    k: int
+    cols: int
 
     @property
     def shape(self) -> tuple[int, int]:
-        return (self.rows, self.k)
+        return (self.rows, self.cols)
 
     @property
     def device(self) -> torch.device:
@@ -47,20 +51,33 @@ class PackedWeight:
     def dtype(self) -> torch.dtype:
         return self.data.dtype
 
-    def to(self, device) -> "PackedWeight":
-        return PackedWeight(self.data.to(device), self.rows, self.k)
+    def to(self, device) -> "PackedMatrix":
+        return PackedMatrix(self.data.to(device), self.rows, self.cols)
+
+    def view_rows(self, rows: int) -> "PackedMatrix":
+        """The first ``rows`` rows (same storage)."""
+        _lib.require(-(-rows // 16) * 16 * self.cols <= self.data.numel(), "PackedMatrix.view_rows: beyond the buffer")
+        return PackedMatrix(self.data, rows, self.cols)
 
     def unpack(self) -> torch.Tensor:
-        """The row-major ``[rows, k]`` weight again (a view permutation; any device)."""
+        """The row-major ``[rows, cols]`` matrix again (a view permutation; any device)."""
         tiles = -(-self.rows // 16)
-        v = self.data.view(tiles, self.k // 128, 4, 4, 16, 8)  # [tile, step, block, g, r, 8]
-        return v.permute(0, 4, 1, 2, 3, 5).reshape(tiles * 16, self.k)[: self.rows].contiguous()
+        v = self.data[: tiles * 16 * self.cols].view(tiles, self.cols // 128, 4, 4, 16, 8)  # [tile, step, block, g, r, 8]
+        return v.permute(0, 4, 1, 2, 3, 5).reshape(tiles * 16, self.cols)[: self.rows].contiguous()
 
 
-Weight = torch.Tensor | PackedWeight
+PackedWeight = PackedMatrix  # a packed weight: rows = output features, cols = k
+Weight = torch.Tensor | PackedMatrix
+Rows = torch.Tensor | PackedMatrix
 
 
-def pack_weight(w: torch.Tensor) -> PackedWeight:
+def packed_rows(rows: int, cols: int, device) -> PackedMatrix:
+    """A zero-filled packed ``[rows, cols]`` bf16 buffer (cols a multiple of 128)."""
+    _lib.require(cols % 128 == 0, "packed_rows: cols must be a multiple of 128")
+    return PackedMatrix(torch.zeros(-(-rows // 16) * 16 * cols, dtype=torch.bfloat16, device=device), rows, cols)
+
+
+def pack_weight(w: torch.Tensor) -> PackedMatrix:
     """Re-order a row-major bf16 ``[rows, k]`` weight (k a multiple of 128) on its GPU."""
     device = _lib.require_gpu(w, name="pack_weight")
     _lib.require(w.dtype == torch.bfloat16 and w.dim() == 2 and w.is_contiguous(), "pack_weight: contiguous bf16 [rows, k]")
@@ -68,62 +85,83 @@ def pack_weight(w: torch.Tensor) -> PackedWeight:
     _lib.require(k % 128 == 0, "pack_weight: k must be a multiple of 128")
     data = torch.empty(int(_lib.lib().oxr_packed_weight_elems(rows, k)), dtype=torch.bfloat16, device=device)
     _lib.call("oxr_pack_weight_bf16", w.data_ptr(), rows, k, data.data_ptr(), _lib.stream(device))
-    return PackedWeight(data, rows, k)
+    return PackedMatrix(data, rows, k)
+
 
 EPI_STORE, EPI_SILU_MUL, EPI_ADD_RESIDUAL = 0, 1, 3
+X_PACKED, Y_PACKED = 1, 2  # OXR_GEMM_X_PACKED, OXR_GEMM_Y_PACKED
 MAX_ROWS = 64  # token rows per launch; larger inputs are processed in slices
 
 
-def _check(x: torch.Tensor, w: Weight, name: str) -> torch.device:
-    wt = w.data if isinstance(w, PackedWeight) else w
-    device = _lib.require_gpu(x, wt, name=name)
-    _lib.require(x.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16, f"{name}: bf16 operands required")
-    _lib.require(x.dim() == 2 and len(w.shape) == 2 and x.shape[1] == w.shape[1], f"{name}: x [m, k] and w [n, k] required")
-    _lib.require(x.stride(1) == 1 and wt.is_contiguous(), f"{name}: rows must be contiguous")
+def _tensor(a: Weight) -> torch.Tensor:
+    return a.data if isinstance(a, PackedMatrix) else a
+
+
+def _check(x: Rows, w: Weight, name: str) -> torch.device:
+    xt, wt = _tensor(x), _tensor(w)
+    device = _lib.require_gpu(xt, wt, name=name)
+    _lib.require(xt.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16, f"{name}: bf16 operands required")
+    _lib.require(len(x.shape) == 2 and len(w.shape) == 2 and x.shape[1] == w.shape[1],
+                 f"{name}: x [m, k] and w [n, k] required")
+    _lib.require(xt.stride(-1) == 1 and wt.is_contiguous(), f"{name}: rows must be contiguous")
     _lib.require(x.shape[1] % 128 == 0, f"{name}: k must be a multiple of 128")
+    _lib.require(not isinstance(x, PackedMatrix) or isinstance(w, PackedMatrix), f"{name}: packed x needs a packed w")
     return device
 
 
-def _entry(name: str, w: Weight) -> str:
-    return name + "_packed" if isinstance(w, PackedWeight) else name
-
-
-def _ptr(w: Weight) -> int:
-    return w.data.data_ptr() if isinstance(w, PackedWeight) else w.data_ptr()
-
-
-def _run(x: torch.Tensor, w: Weight, n: int, epilogue: int, y: torch.Tensor, device: torch.device) -> None:
+def _run(x: Rows, w: Weight, n: int, epilogue: int, y: Rows, device: torch.device) -> None:
     m = x.shape[0]
+    if isinstance(w, PackedMatrix):
+        flags = (X_PACKED if isinstance(x, PackedMatrix) else 0) | (Y_PACKED if isinstance(y, PackedMatrix) else 0)
+        if flags:
+            _lib.require(m <= MAX_ROWS, "packed rows: at most 64 per call")
+        ldx = 0 if isinstance(x, PackedMatrix) else x.stride(0)
+        ldy = 0 if isinstance(y, PackedMatrix) else y.stride(0)
+        for start in range(0, m, MAX_ROWS):
+            rows = min(MAX_ROWS, m - start)
+            xp = x.data.data_ptr() if isinstance(x, PackedMatrix) else x[start:].data_ptr()
+            yp = y.data.data_ptr() if isinstance(y, PackedMatrix) else y[start:].data_ptr()
+            _lib.call("oxr_gemm_bf16_packed", xp, ldx, rows, w.data.data_ptr(), w.shape[1], n, epilogue, yp, ldy,
+                      flags, _lib.stream(device))
+        return
+    _lib.require(not isinstance(y, PackedMatrix), "packed output needs a packed w")
     for start in range(0, m, MAX_ROWS):
         rows = min(MAX_ROWS, m - start)
-        _lib.call(_entry("oxr_gemm_bf16", w), x[start:].data_ptr(), x.stride(0), rows, _ptr(w), w.shape[1], n,
-                  epilogue, y[start:].data_ptr(), y.stride(0), _lib.stream(device))
+        _lib.call("oxr_gemm_bf16", x[start:].data_ptr(), x.stride(0), rows, w.data_ptr(), w.shape[1], n, epilogue,
+                  y[start:].data_ptr(), y.stride(0), _lib.stream(device))
 
 
-def linear(x: torch.Tensor, w: Weight, out: torch.Tensor | None = None) -> torch.Tensor:
+def _check_out(out: Rows, m: int, n: int, name: str) -> None:
+    if isinstance(out, PackedMatrix):
+        _lib.require(out.shape == (m, n) and out.data.numel() >= -(-m // 16) * 16 * n, f"{name}: packed out too small")
+    else:
+        _lib.require(out.shape == (m, n) and out.stride(1) == 1, f"{name}: out must be [m, n] with contiguous rows")
+
+
+def linear(x: Rows, w: Weight, out: Rows | None = None) -> Rows:
     """``x @ w.T`` in bf16 with fp32 accumulation (``F.linear`` without bias)."""
     device = _check(x, w, "linear")
     n = w.shape[0]
     if out is None:
         out = torch.empty(x.shape[0], n, dtype=torch.bfloat16, device=device)
-    _lib.require(out.shape == (x.shape[0], n) and out.stride(1) == 1, "linear: out must be [m, n] with contiguous rows")
+    _check_out(out, x.shape[0], n, "linear")
     _run(x, w, n, EPI_STORE, out, device)
     return out
 
 
-def linear_silu_mul(x: torch.Tensor, w: Weight, out: torch.Tensor | None = None) -> torch.Tensor:
+def linear_silu_mul(x: Rows, w: Weight, out: Rows | None = None) -> Rows:
     """``silu(g) * u`` where ``[g | u] = x @ w.T`` (``w`` is the fused gate_up weight, gate rows first)."""
     device = _check(x, w, "linear_silu_mul")
     _lib.require(w.shape[0] % 2 == 0, "linear_silu_mul: w must hold gate and up rows")
     n = w.shape[0] // 2
     if out is None:
         out = torch.empty(x.shape[0], n, dtype=torch.bfloat16, device=device)
-    _lib.require(out.shape == (x.shape[0], n) and out.stride(1) == 1, "linear_silu_mul: out must be [m, n]")
+    _check_out(out, x.shape[0], n, "linear_silu_mul")
     _run(x, w, n, EPI_SILU_MUL, out, device)
     return out
 
 
-def linear_add_(residual: torch.Tensor, x: torch.Tensor, w: Weight) -> torch.Tensor:
+def linear_add_(residual: torch.Tensor, x: Rows, w: Weight) -> torch.Tensor:
     """``residual = bf16(bf16(x @ w.T) + residual)``, in place; returns ``residual``."""
     device = _check(x, w, "linear_add_")
     n = w.shape[0]
@@ -138,7 +176,7 @@ def partial_splits(n: int, k: int) -> int:
     return int(_lib.lib().oxr_gemm_bf16_partial_splits(n, k))
 
 
-def linear_partial(x: torch.Tensor, w: Weight, partials: torch.Tensor) -> int:
+def linear_partial(x: Rows, w: Weight, partials: torch.Tensor) -> int:
     """fp32 partial sums of ``x @ w.T`` over ``partial_splits(n, k)`` k slices into
     ``partials[:splits, :m, :n]``; returns the number of slices."""
     device = _check(x, w, "linear_partial")
@@ -147,17 +185,25 @@ def linear_partial(x: torch.Tensor, w: Weight, partials: torch.Tensor) -> int:
     splits = partial_splits(n, k)
     _lib.require(partials.dtype == torch.float32 and partials.is_contiguous() and partials.numel() >= splits * m * n,
                  "linear_partial: partials must be contiguous fp32 with room for splits * m * n")
-    _lib.call(_entry("oxr_gemm_bf16_partial", w), x.data_ptr(), x.stride(0), m, _ptr(w), k, n, partials.data_ptr(),
-              splits, _lib.stream(device))
+    if isinstance(w, PackedMatrix):
+        xp = isinstance(x, PackedMatrix)
+        _lib.call("oxr_gemm_bf16_partial_packed", _tensor(x).data_ptr(), 0 if xp else x.stride(0), m,
+                  w.data.data_ptr(), k, n, partials.data_ptr(), splits, X_PACKED if xp else 0, _lib.stream(device))
+    else:
+        _lib.call("oxr_gemm_bf16_partial", x.data_ptr(), x.stride(0), m, w.data_ptr(), k, n, partials.data_ptr(),
+                  splits, _lib.stream(device))
     return splits
 
 
 def add_partials_rms_norm(partials: torch.Tensor, splits: int, residual: torch.Tensor, weight: torch.Tensor,
-                          eps: float, out: torch.Tensor) -> torch.Tensor:
+                          eps: float, out: Rows) -> Rows:
     """``residual = bf16(bf16(sum of partials) + residual)``; ``out = rms_norm(residual) * weight``
-    (``_add_rms_norm``, language.py:94-99, taking a ``linear_partial`` result)."""
-    device = _lib.require_gpu(partials, residual, weight, out, name="add_partials_rms_norm")
+    (``_add_rms_norm``, language.py:94-99, taking a ``linear_partial`` result).  ``out`` may be a
+    :class:`PackedMatrix` (the next GEMM's packed x)."""
+    device = _lib.require_gpu(partials, residual, weight, _tensor(out), name="add_partials_rms_norm")
     rows, hidden = residual.shape
+    _check_out(out, rows, hidden, "add_partials_rms_norm")
     _lib.call("oxr_add_partials_rms_norm", partials.data_ptr(), splits, rows, hidden, residual.data_ptr(),
-              weight.data_ptr(), float(eps), out.data_ptr(), _lib.stream(device))
+              weight.data_ptr(), float(eps), _tensor(out).data_ptr(), 1 if isinstance(out, PackedMatrix) else 0,
+              _lib.stream(device))
     return out

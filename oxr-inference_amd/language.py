@@ -161,10 +161,11 @@ class StepBuffers:
     """Every intermediate of one forward, allocated once for up to ``max_tokens`` rows."""
 
     residual: torch.Tensor
-    h: torch.Tensor
+    h: torch.Tensor                 # row-major: the final norm's output (the LM head's input)
+    h_packed: gemm.PackedMatrix     # the layers' norm outputs, packed x of qkv / gate_up
     qkv: torch.Tensor
-    attn: torch.Tensor
-    act: torch.Tensor
+    attn: gemm.PackedMatrix         # [B * S, H * D] packed x of o_proj
+    act: gemm.PackedMatrix          # [B * S, intermediate] packed x of down_proj
     attn_workspace: torch.Tensor
     head_workspace: torch.Tensor
     predicted: torch.Tensor
@@ -181,9 +182,10 @@ class StepBuffers:
         bf = dict(dtype=torch.bfloat16, device=device)
         return cls(
             residual=torch.zeros(t, config.hidden_size, **bf), h=torch.zeros(t, config.hidden_size, **bf),
+            h_packed=gemm.packed_rows(t, config.hidden_size, device),
             qkv=torch.zeros(t, config.qkv_size, **bf),
-            attn=torch.zeros(max_batch, tokens_per_seq, config.num_heads, config.head_dim, **bf),
-            act=torch.zeros(t, config.intermediate_size, **bf),
+            attn=gemm.packed_rows(t, config.num_heads * config.head_dim, device),
+            act=gemm.packed_rows(t, config.intermediate_size, device),
             attn_workspace=torch.zeros(max(attention.workspace_bytes(max_batch, config.num_kv_heads, max_seq_len), 1),
                                        dtype=torch.uint8, device=device),
             head_workspace=torch.zeros(max(lm_head.workspace_bytes(t, config.vocab_size), 1), dtype=torch.uint8,
@@ -228,23 +230,29 @@ class LanguageModel:
         buffers.pending_splits = 0
         c, w = self.config, self.weights
         t = batch.block_table.shape[0] * batch.tokens_per_seq
-        res, h = buffers.residual[:t], buffers.h[:t]
+        res = buffers.residual[:t]
         stream = _lib.stream(batch.positions.device)
         if batch.ids is not None:
             _lib.call("oxr_embed_rms_norm", batch.ids.data_ptr(), t, w.embed.data_ptr(), c.vocab_size, c.hidden_size,
-                      w.layers[0].input_norm.data_ptr(), float(c.rms_norm_eps), res.data_ptr(), h.data_ptr(), stream)
+                      w.layers[0].input_norm.data_ptr(), float(c.rms_norm_eps), res.data_ptr(),
+                      buffers.h_packed.data.data_ptr(), 1, stream)
         else:
             res.copy_(batch.embeds)
-            self._norm(res, w.layers[0].input_norm, h, stream)
+            self._norm(res, w.layers[0].input_norm, buffers.h_packed.view_rows(t), stream)
 
-    def _norm(self, x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, stream: int) -> None:
+    def _norm(self, x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | gemm.PackedMatrix, stream: int) -> None:
         c = self.config
+        packed = isinstance(out, gemm.PackedMatrix)
         _lib.call("oxr_rms_norm", x.data_ptr(), x.stride(0), x.shape[0], c.hidden_size, weight.data_ptr(),
-                  float(c.rms_norm_eps), out.data_ptr(), out.stride(0), stream)
+                  float(c.rms_norm_eps), out.data.data_ptr() if packed else out.data_ptr(),
+                  0 if packed else out.stride(0), 1 if packed else 0, stream)
 
-    def _settle_norm(self, buffers: StepBuffers, t: int, weight: torch.Tensor, stream: int) -> None:
-        """h = rms_norm(residual) * weight, first adding any pending GEMM partials to the residual."""
-        res, h = buffers.residual[:t], buffers.h[:t]
+    def _settle_norm(self, buffers: StepBuffers, t: int, weight: torch.Tensor, stream: int, *,
+                     packed: bool = True) -> None:
+        """h = rms_norm(residual) * weight, first adding any pending GEMM partials to the residual;
+        into ``buffers.h_packed`` (the next layer GEMM's x) or, with ``packed=False``, ``buffers.h``."""
+        res = buffers.residual[:t]
+        h = buffers.h_packed.view_rows(t) if packed else buffers.h[:t]
         if buffers.pending_splits:
             gemm.add_partials_rms_norm(buffers.partials, buffers.pending_splits, res, weight,
                                        self.config.rms_norm_eps, h)
@@ -261,10 +269,9 @@ class LanguageModel:
         b, s = batch.block_table.shape[0], batch.tokens_per_seq
         t = b * s
         stream = _lib.stream(batch.positions.device)
-        h = buffers.h[:t]
+        h = buffers.h_packed.view_rows(t)
         qkv = buffers.qkv[:t]
-        attn, act = buffers.attn[:b], buffers.act[:t]
-        attn_flat = attn.view(t, c.num_heads * c.head_dim)
+        attn, act = buffers.attn.view_rows(t), buffers.act.view_rows(t)
         max_seq_len = min(buffers.max_seq_len, batch.block_table.shape[1] * cache.block_size)
         eps = float(c.rms_norm_eps)
         for index in range(start, stop):
@@ -278,19 +285,20 @@ class LanguageModel:
                 batch.slots, batch.seq_lens, batch.block_table, c.num_heads, scale=c.head_dim ** -0.5,
                 max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace,
             )
-            buffers.pending_splits = gemm.linear_partial(attn_flat, layer.o, buffers.partials)
+            buffers.pending_splits = gemm.linear_partial(attn, layer.o, buffers.partials)
             self._settle_norm(buffers, t, layer.post_norm, stream)
             gemm.linear_silu_mul(h, layer.gate_up, out=act)
             buffers.pending_splits = gemm.linear_partial(act, layer.down, buffers.partials)
 
-    def settle(self, batch: ExtendBatch, buffers: StepBuffers, weight: torch.Tensor) -> None:
-        """Add pending partials to the residual (and normalise it with ``weight`` into ``h``)."""
+    def settle(self, batch: ExtendBatch, buffers: StepBuffers, weight: torch.Tensor, *, packed: bool = True) -> None:
+        """Add pending partials to the residual (and normalise it with ``weight`` into
+        ``h_packed``, or ``h`` with ``packed=False``)."""
         t = batch.block_table.shape[0] * batch.tokens_per_seq
-        self._settle_norm(buffers, t, weight, _lib.stream(batch.positions.device))
+        self._settle_norm(buffers, t, weight, _lib.stream(batch.positions.device), packed=packed)
 
     def final_norm(self, batch: ExtendBatch, buffers: StepBuffers) -> torch.Tensor:
         t = batch.block_table.shape[0] * batch.tokens_per_seq
-        self._settle_norm(buffers, t, self.weights.final_norm, _lib.stream(batch.positions.device))
+        self._settle_norm(buffers, t, self.weights.final_norm, _lib.stream(batch.positions.device), packed=False)
         return buffers.h[:t]
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:

@@ -80,4 +80,9 @@ def test_entry_points_reject_bad_arguments_before_launch() -> None:
     assert lib.oxr_pack_weight_bf16(None, 32, 128, 4096, None) == -1  # no source
     assert lib.oxr_pack_weight_bf16(4096, 32, 128, 4096 + 64, None) == -1  # overlapping buffers
     # packed SiLU*mul needs the up rows to start a tile (n % 16 == 0)
-    assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 40, 1, 4096, 40, None) == -2
+    assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 40, 1, 4096, 40, 0, None) == -2
+    assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 64, 0, 4096, 64, 4, None) == -1  # unknown flag
+    # packed y needs a row length that is a multiple of 128, and no residual add
+    assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 64, 0, 4096, 0, 2, None) == -2
+    assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 128, 3, 4096, 0, 2, None) == -2
+    assert lib.oxr_gemm_bf16_partial_packed(16, 0, 4, 32, 128, 64, 4096, 1, 2, None) == -1  # y flag on partials

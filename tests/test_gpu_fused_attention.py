@@ -17,6 +17,7 @@ from conftest import announce, pkg
 
 pytestmark = pytest.mark.gpu
 attention = pkg("attention")
+gemm = pkg("gemm")
 _lib = pkg("_lib")
 
 
@@ -63,7 +64,13 @@ def _case(seq_lens, S, H, KV, block_size, seed, bad_slot=False):
     # Fused.
     k2, v2 = kc.clone(), vc.clone()
     out2 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k2, v2, slots_t, seq_t, table_t, H)
+    # Fused, output packed for the o_proj GEMM: the same values.
+    k3, v3 = kc.clone(), vc.clone()
+    out3 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k3, v3, slots_t, seq_t, table_t, H,
+                                               out=gemm.packed_rows(B * S, H * 128, dev))
     torch.cuda.synchronize()
+    assert torch.equal(out2.view(torch.int16).view(B * S, H * 128), out3.unpack().view(torch.int16)), "packed output"
+    assert torch.equal(k2.view(torch.int16), k3.view(torch.int16)) and torch.equal(v2.view(torch.int16), v3.view(torch.int16))
     if bad_slot:
         # The row with no valid slot is not stored by either path; the fused kernel still attends to
         # the token's computed row, the separate calls to whatever the cache held.  Sequence 0 owns

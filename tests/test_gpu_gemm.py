@@ -20,6 +20,7 @@ from oracle import bf16, lm_head as oracle_lm_head
 pytestmark = pytest.mark.gpu
 gemm = pkg("gemm")
 lm_head = pkg("lm_head")
+_lib = pkg("_lib")
 
 ATOL, RTOL = 2e-2, 1e-2
 
@@ -149,6 +150,67 @@ def test_packed_weight_gemm_bit_identical(m: int, k: int, n: int, epi: str) -> N
         a, b = fn(x, w), fn(x, p)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,k,n,epi", [(32, 2048, 4096, "store"), (32, 2048, 6144, "silu"), (32, 2048, 2048, "partial"),
+                                       (32, 6144, 2048, "partial"), (7, 256, 128, "store"), (20, 512, 256, "silu"),
+                                       (17, 128, 40, "partial")])
+def test_packed_rows_bit_identical(m: int, k: int, n: int, epi: str) -> None:
+    """Token rows in the packed layout (x read packed, y written packed) give the row-major results
+    bit for bit; rows past m in the last tile are padding and may hold anything."""
+    g = torch.Generator(device="cuda").manual_seed(3 * m + k + n)
+    x = _rand(g, m, k)
+    w = gemm.pack_weight(_rand(g, 2 * n if epi == "silu" else n, k, std=0.02))
+    xp = gemm.pack_weight(x)  # the same layout as packed token rows
+    if m % 16:  # poison the last tile's padding rows: their results must never be stored
+        tiles = -(-m // 16)
+        xp.data.view(tiles, k // 128, 4, 4, 16, 8)[-1, :, :, :, m % 16:, :] = float("nan")
+    announce("packed rows", m, k, n, epi)
+    if epi == "partial":
+        splits = gemm.partial_splits(n, k)
+        a = torch.full((splits, m, n), float("nan"), device="cuda")
+        b = torch.full((splits, m, n), float("nan"), device="cuda")
+        gemm.linear_partial(x, w, a)
+        gemm.linear_partial(xp, w, b)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+        return
+    fn = gemm.linear if epi == "store" else gemm.linear_silu_mul
+    a = fn(x, w)
+    b = fn(xp, w, out=gemm.packed_rows(m, n, "cuda"))
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.unpack().view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,hidden", [(32, 2048), (12, 512), (40, 1024)])
+def test_norms_packed_output(rows: int, hidden: int) -> None:
+    """The three norm entry points write the same values packed as row-major."""
+    g = torch.Generator(device="cuda").manual_seed(rows + hidden)
+    lib = _lib
+    st = lib.stream(torch.device("cuda"))
+    x, wn = _rand(g, rows, hidden), (0.5 + torch.rand(hidden, generator=g, device="cuda")).to(torch.bfloat16)
+    announce("norms packed", rows, hidden)
+    a = torch.empty(rows, hidden, dtype=torch.bfloat16, device="cuda")
+    b = gemm.packed_rows(rows, hidden, "cuda")
+    lib.call("oxr_rms_norm", x.data_ptr(), hidden, rows, hidden, wn.data_ptr(), 1e-6, a.data_ptr(), hidden, 0, st)
+    lib.call("oxr_rms_norm", x.data_ptr(), hidden, rows, hidden, wn.data_ptr(), 1e-6, b.data.data_ptr(), 0, 1, st)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.unpack().view(torch.int16))
+    table = _rand(g, 100, hidden)
+    ids = torch.randint(0, 100, (rows,), generator=g, device="cuda")
+    ra, rb = torch.empty_like(a), torch.empty_like(a)
+    lib.call("oxr_embed_rms_norm", ids.data_ptr(), rows, table.data_ptr(), 100, hidden, wn.data_ptr(), 1e-6,
+             ra.data_ptr(), a.data_ptr(), 0, st)
+    lib.call("oxr_embed_rms_norm", ids.data_ptr(), rows, table.data_ptr(), 100, hidden, wn.data_ptr(), 1e-6,
+             rb.data_ptr(), b.data.data_ptr(), 1, st)
+    torch.cuda.synchronize()
+    assert torch.equal(ra, rb) and torch.equal(a.view(torch.int16), b.unpack().view(torch.int16))
+    parts = torch.randn(4, rows, hidden, generator=g, device="cuda")
+    r1, r2 = x.clone(), x.clone()
+    gemm.add_partials_rms_norm(parts, 4, r1, wn, 1e-6, a)
+    gemm.add_partials_rms_norm(parts, 4, r2, wn, 1e-6, b)
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2) and torch.equal(a.view(torch.int16), b.unpack().view(torch.int16))
 
 
 @pytest.mark.parametrize("m,vocab,k", [(32, 151_936, 2048), (8, 4096 + 40, 2048), (40, 1000, 512), (3, 72, 384)])
