@@ -8,16 +8,18 @@
 //
 // Work split.  A verify step has only B * KV (sequence, kv-head) pairs, each
 // with R = S * (H / KV) query rows (8 at S=4, 16/8 heads), against contexts
-// of thousands of tokens.  Each pair's context is cut into `splits` ranges so
-// that about 256 workgroups (one per CU) cover the batch; a workgroup is 8
-// waves that walk its range in interleaved 32-key steps (the 8 waves read
-// neighbouring keys of the same pages at the same time).  The 8 waves'
-// (max, sum, O) are merged on chip through LDS and written as the split's
-// partial; a second small kernel merges the splits.  (A "last workgroup
-// merges" scheme in one kernel needs a device-scope release/acquire per
-// workgroup, i.e. an L2 writeback + invalidate across XCDs, which measured
-// ~70 us per launch here -- far more than a second launch.)  A context that
-// fits one split is stored directly by the main kernel.
+// of thousands of tokens.  A workgroup of 8 waves owns HPW adjacent kv heads
+// (2 when the fused row jobs fit, else 1) of one sequence and one of `splits`
+// ranges of its context, so that about 256 workgroups (one per CU) cover the
+// batch.  Each head gets 8 / HPW waves that walk the range in interleaved
+// 32-key steps; at any time the workgroup reads neighbouring keys of the same
+// pages, HPW adjacent 256-byte head slices of each 2 KB token row.  A head's
+// waves' (max, sum, O) are merged on chip through LDS and written as the
+// split's partial; a second small kernel merges the splits.  (A "last
+// workgroup merges" scheme in one kernel needs a device-scope acquire-release
+// per workgroup, i.e. an L2 writeback + invalidate across XCDs, which costs
+// more than the second launch.)  A context that fits one split is stored
+// directly by the main kernel.
 //
 // Per wave, 32 keys at a time (two 16-key MFMA tiles), all in registers:
 //   S^T tile = K[16 keys x 128] * Q^T           4 v_mfma_f32_16x16x32_bf16 / tile
@@ -37,6 +39,8 @@
 //     standing for key 16p + 4g + j; accumulators hold O^T[d][r], so the
 //     per-row rescale is a per-lane scalar.
 // The next 32 keys' K and V are loaded before the current ones are used.
+#include <algorithm>
+
 #include "norm_rope.h"
 
 namespace oxr {
@@ -128,52 +132,60 @@ struct RopeArgs {
 // workgroup whose key range holds their positions, before any wave reads them;
 // otherwise q is read as given.  The caches are plain (not restrict) pointers
 // because the fused kernel writes the rows it later reads.
-template <bool kFused>
+template <bool kFused, int HPW>
 __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const bf16_t* __restrict__ q, const bf16_t* k_cache, const bf16_t* v_cache, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ block_table, int64_t table_stride, int S, int H, int KV, int log2_bs,
     int64_t num_blocks, float scale_log2, int max_seq_len, int splits, float* __restrict__ part_o,
     float* __restrict__ part_ml, bf16_t* __restrict__ out, int out_packed, RopeArgs ra) {
+  constexpr int kStreams = kWaves / HPW;  // waves per kv head
   __shared__ float s_o[kWaves][kRows][kD];
-  __shared__ u32x4 s_q[kFused ? kRows : 1][kD / 8];
-  __shared__ u32x4 s_newk[kFused ? kMaxNew : 1][kD / 8], s_newv[kFused ? kMaxNew : 1][kD / 8];
+  __shared__ u32x4 s_q[kFused ? HPW : 1][kFused ? kRows : 1][kD / 8];
+  __shared__ u32x4 s_newk[kFused ? HPW : 1][kFused ? kMaxNew : 1][kD / 8];
+  __shared__ u32x4 s_newv[kFused ? HPW : 1][kFused ? kMaxNew : 1][kD / 8];
   __shared__ float s_m[kWaves][kRows], s_l[kWaves][kRows];
   __shared__ int s_pages[kMaxSpanPages];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, b = blockIdx.z;
   const int G = H / KV, R = S * G;
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, so its addressing is scalar
   const int r = lane & 15, g = lane >> 4;
+  // The workgroup owns kv heads [HPW * blockIdx.y, +HPW): wave w serves head
+  // slot w % HPW and walks that head's keys as stream w / HPW of kStreams.
+  const int hs = wave % HPW, stream = wave / HPW;
+  const int kvh = (int)blockIdx.y * HPW + hs;
 
-  // Fused: 32 jobs of one 128-element row on 16 lanes -- q rows [0, R), then
-  // the K rows and the V rows of the S new tokens.  Lanes without a job redo
-  // row 0 (every lane must take part in the norm's exchanges) and store
-  // nothing.  Their loads go out first: none depends on the context length.
-  int f_job = 0, f_s16 = 0, f_jk = 0, f_jv = 0, f_jend = 0, f_jj = 0, f_ss = 0;
+  // Fused: HPW * (R + 2S) <= 32 jobs of one 128-element row on 16 lanes --
+  // per head slot, q rows [0, R), then the K rows and the V rows of the S new
+  // tokens.  Lanes without a job redo job 0 (every lane must take part in the
+  // norm's exchanges) and store nothing.  Their loads go out first: none
+  // depends on the context length.
+  const int f_s16 = tid & 15, f_job = tid >> 4;
+  const int f_per_head = R + 2 * S;
+  const bool f_valid = f_job < HPW * f_per_head;
+  int f_hs = 0, f_jj = 0, f_ss = 0;
   int64_t f_trow = 0, f_slot = -1;
   u32x4 f_raw = {0u, 0u, 0u, 0u}, f_w8 = {0u, 0u, 0u, 0u};
   if constexpr (kFused) {
-    f_job = tid >> 4;
-    f_s16 = tid & 15;
-    f_jk = R;
-    f_jv = R + S;
-    f_jend = R + 2 * S;
-    f_jj = f_job < f_jend ? f_job : 0;
+    const int jv = f_valid ? f_job : 0;
+    f_hs = jv / f_per_head;
+    f_jj = jv % f_per_head;
+    const int kvh_j = (int)blockIdx.y * HPW + f_hs;
     int head;
-    if (f_jj < f_jk) {
+    if (f_jj < R) {
       f_ss = f_jj / G;
-      head = kvh * G + f_jj % G;
-    } else if (f_jj < f_jv) {
-      f_ss = f_jj - f_jk;
-      head = H + kvh;
+      head = kvh_j * G + f_jj % G;
+    } else if (f_jj < R + S) {
+      f_ss = f_jj - R;
+      head = H + kvh_j;
     } else {
-      f_ss = f_jj - f_jv;
-      head = H + KV + kvh;
+      f_ss = f_jj - R - S;
+      head = H + KV + kvh_j;
     }
     const int64_t tok = (int64_t)b * S + f_ss;
     f_raw = ld128(ra.qkv + (tok * (H + 2 * KV) + head) * kD + f_s16 * 8);
-    f_w8 = ld128((f_jj < f_jk ? ra.q_weight : ra.k_weight) + f_s16 * 8);
+    f_w8 = ld128((f_jj < R ? ra.q_weight : ra.k_weight) + f_s16 * 8);
     f_slot = ra.slots[tok];
     f_trow = ra.positions[tok];
   }
@@ -196,12 +208,13 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   const int64_t my_page = table_row[npages > 0 ? page0 + min(tid, npages - 1) : 0];
   __builtin_amdgcn_sched_barrier(0);
 
-  // The waves take pairs wave, wave + 8, ... so at any time the workgroup reads
-  // 8 neighbouring pairs of the same pages.  Each wave's first pair is requested
-  // right away, its pages read straight from the table, so it is in flight
-  // during the page-table staging, the fused q/k work and the barrier.
-  const int stride = 32 * kWaves;
-  const int t_first = t_begin + 32 * wave;
+  // A head's streams take pairs stream, stream + kStreams, ... so at any time
+  // the workgroup reads neighbouring pairs of the same pages, HPW adjacent
+  // head slices of each token row.  Each wave's first pair is requested right
+  // away, its pages read straight from the table, so it is in flight during
+  // the page-table staging, the fused q/k work and the barrier.
+  const int stride = 32 * kStreams;
+  const int t_first = t_begin + 32 * stream;
   const int n = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
   // (Issued by every wave -- a wave without pairs reads a valid row it never
   // uses -- so that no branch blurs the wait counts that follow.)
@@ -235,19 +248,21 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   if constexpr (kFused) {
     // The new tokens' rows (see the top of the kernel for the job layout).
     const u32x4 normed = norm_rope_16v(f_raw, f_w8, f_c8, f_s8, ra.eps, f_s16);
-    if (f_job < f_jk) {
-      s_q[f_jj][f_s16] = normed;
-    } else if (f_job < f_jend) {
+    if (f_valid && f_jj < R) {
+      s_q[f_hs][f_jj][f_s16] = normed;
+    } else if (f_valid) {
       // Kept in LDS for this workgroup's own reads of the new rows, and
       // written to the cache by the workgroup whose keys hold the token's
       // position (each row stored once; nothing in this launch reads it back
       // from memory, so the stores need not complete before the loop).
-      if (f_job < f_jv) s_newk[f_ss][f_s16] = normed;
-      else s_newv[f_ss][f_s16] = f_raw;
+      const bool is_k = f_jj < R + S;
+      if (is_k) s_newk[f_hs][f_ss][f_s16] = normed;
+      else s_newv[f_hs][f_ss][f_s16] = f_raw;
       const int pos = L - S + f_ss;
       if (pos >= t_begin && pos < t_end && f_slot >= 0 && f_slot < ra.num_slots) {
-        bf16_t* dst = (f_job < f_jv ? ra.k_store : ra.v_store) + (f_slot * KV + kvh) * kD + f_s16 * 8;
-        st128(dst, f_job < f_jv ? normed : f_raw);
+        const int kvh_j = (int)blockIdx.y * HPW + f_hs;
+        bf16_t* dst = (is_k ? ra.k_store : ra.v_store) + (f_slot * KV + kvh_j) * kD + f_s16 * 8;
+        st128(dst, is_k ? normed : f_raw);
       }
     }
   }
@@ -275,7 +290,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   if constexpr (kFused) {
     if (r < R) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qf[i] = s_q[r][4 * i + g];
+      for (int i = 0; i < 4; ++i) qf[i] = s_q[hs][r][4 * i + g];
     }
   }
 
@@ -294,9 +309,9 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
           const int ns = min(t0 + 16 * p + r, L - 1) - (L - S);  // keys past L re-read row L - 1
           if (ns >= 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) cur.k[p][i] = s_newk[ns][4 * i + g];  // dims 32i + 8g
+            for (int i = 0; i < 4; ++i) cur.k[p][i] = s_newk[hs][ns][4 * i + g];  // dims 32i + 8g
 #pragma unroll
-            for (int c = 0; c < 4; ++c) cur.v[p][c] = s_newv[ns][4 * c + g];  // dims 32c + 8g
+            for (int c = 0; c < 4; ++c) cur.v[p][c] = s_newv[hs][ns][4 * c + g];  // dims 32c + 8g
           }
         }
       }
@@ -380,7 +395,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     }
   }
 
-  // Merge the 8 waves on chip.
+  // Merge each head's kStreams waves on chip.
   float l_tot = l_run + shfl_xor_f(l_run, 16);
   l_tot += shfl_xor_f(l_tot, 32);
 #pragma unroll
@@ -390,17 +405,19 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     s_l[wave][r] = l_tot;
   }
   __syncthreads();
-  const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
-  for (int idx = tid; idx < R * (kD / 4); idx += 64 * kWaves) {
-    const int rr = idx / (kD / 4), d0 = (idx % (kD / 4)) * 4;
+  for (int idx = tid; idx < HPW * R * (kD / 4); idx += 64 * kWaves) {
+    const int ho = idx / (R * (kD / 4)), rr = (idx / (kD / 4)) % R, d0 = (idx % (kD / 4)) * 4;
+    const int kvh_o = (int)blockIdx.y * HPW + ho;
+    const int64_t unit0 = ((int64_t)b * KV + kvh_o) * splits;
     float mmax = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, s_m[w][rr]);
+    for (int k = 0; k < kStreams; ++k) mmax = fmaxf(mmax, s_m[ho + HPW * k][rr]);
     const float mu = (mmax == -INFINITY) ? 0.f : mmax;
     float l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int k = 0; k < kStreams; ++k) {
+      const int w = ho + HPW * k;
       const float wt = exp2f(s_m[w][rr] - mu);
       l += s_l[w][rr] * wt;
       acc += *reinterpret_cast<const f32x4*>(&s_o[w][rr][d0]) * wt;
@@ -408,7 +425,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     if (single) {
       const float inv = l > 0.f ? 1.0f / l : 0.f;
       const int s = rr / G, hh = rr % G;
-      uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh * G + hh) * kD + d0, H * kD, out_packed);
+      uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh_o * G + hh) * kD + d0, H * kD, out_packed);
       dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
       dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
     } else {
@@ -468,12 +485,32 @@ __global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(cons
   dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
 }
 
-// Context splits per (sequence, kv head): about one 8-wave workgroup per CU
-// over the whole batch.
-int splits_for(int32_t batch, int32_t num_kv_heads) {
-  const int64_t units = (int64_t)batch * num_kv_heads;
+// Context splits per (sequence, group of `hpw` kv heads): about one 8-wave
+// workgroup per CU over the whole batch.
+int splits_for(int32_t batch, int32_t num_kv_heads, int hpw) {
+  const int64_t units = (int64_t)batch * (num_kv_heads / hpw);
   int64_t splits = (256 + units - 1) / units;
   return (int)(splits < 1 ? 1 : (splits > 64 ? 64 : splits));
+}
+
+#ifndef OXR_ATTN_HPW
+#define OXR_ATTN_HPW 0  // 0: choose; 1 or 2: force (for measurement builds)
+#endif
+
+// kv heads per workgroup: two heads read 512-byte slices of each token row
+// together (the heads of a row are adjacent) -- measured 1 us faster per
+// launch than one head at the verify shape; four heads (16 splits) were 3 us
+// slower.  The fused kernel's row jobs must fit one per 16-lane group; the
+// unfused kernel makes the same choice, so that both split the context the
+// same way and give the same bits.
+int pick_hpw(int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads) {
+  const int jobs_per_head = tokens_per_seq * (num_heads / num_kv_heads + 2);
+  for (int hpw : {2, 1}) {
+    if (OXR_ATTN_HPW != 0 && hpw != OXR_ATTN_HPW) continue;
+    if (num_kv_heads % hpw != 0 || hpw * jobs_per_head > 32) continue;
+    return hpw;
+  }
+  return 1;
 }
 
 }  // namespace
@@ -482,7 +519,10 @@ int splits_for(int32_t batch, int32_t num_kv_heads) {
 extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
   using namespace oxr;
   if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0) return 0;
-  const size_t units = (size_t)batch * num_kv_heads * splits_for(batch, num_kv_heads);
+  int splits = 0;  // the most any head grouping uses
+  for (int hpw : {1, 2})
+    if (num_kv_heads % hpw == 0) splits = std::max(splits, splits_for(batch, num_kv_heads, hpw));
+  const size_t units = (size_t)batch * num_kv_heads * splits;
   return units * kRows * (kD + 2) * sizeof(float);
 }
 
@@ -509,7 +549,8 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   const size_t need = oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
   OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535 || num_blocks > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
-  const int splits = splits_for(batch, num_kv_heads);
+  const int hpw = pick_hpw(tokens_per_seq, num_heads, num_kv_heads);
+  const int splits = splits_for(batch, num_kv_heads, hpw);
   {
     // One split's page-table range must fit the kernel's LDS copy.
     const int64_t span_max = ((max_seq_len + splits - 1) / splits + 31) / 32 * 32;
@@ -520,15 +561,19 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)batch * num_kv_heads * splits * kRows * kD;
   const float scale_log2 = scale * 1.4426950408889634f;
-  const dim3 grid(splits, num_kv_heads, batch), block(64 * kWaves);
+  const dim3 grid(splits, num_kv_heads / hpw, batch), block(64 * kWaves);
+  const RopeArgs rope = ra ? *ra : RopeArgs{};
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, ra ? nullptr : q, k_cache, v_cache, seq_lens, block_table,
+                       table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
+                       max_seq_len, splits, part_o, part_ml, out, out_packed, rope);
+  };
   if (ra) {
-    hipLaunchKernelGGL(paged_extend_kernel<true>, grid, block, 0, s, nullptr, k_cache, v_cache, seq_lens, block_table,
-                       table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
-                       max_seq_len, splits, part_o, part_ml, out, out_packed, *ra);
+    if (hpw == 2) launch(paged_extend_kernel<true, 2>);
+    else launch(paged_extend_kernel<true, 1>);
   } else {
-    hipLaunchKernelGGL(paged_extend_kernel<false>, grid, block, 0, s, q, k_cache, v_cache, seq_lens, block_table,
-                       table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
-                       max_seq_len, splits, part_o, part_ml, out, out_packed, RopeArgs{});
+    if (hpw == 2) launch(paged_extend_kernel<false, 2>);
+    else launch(paged_extend_kernel<false, 1>);
   }
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;

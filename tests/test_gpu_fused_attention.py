@@ -99,6 +99,13 @@ def test_block_256_and_skipped_slot() -> None:
     _case([700, 257, 1300, 90], 4, 16, 8, 256, seed=12, bad_slot=True)
 
 
+def test_eight_new_tokens_long_contexts() -> None:
+    """S=8 (one kv head per workgroup) at contexts long enough for every split to hold keys."""
+    lens = [4100, 2600, 700, 5000]
+    announce(f"fused attention S=8 lens={lens}")
+    _case(lens, 8, 16, 8, 16, seed=14)
+
+
 def test_single_sequence_many_splits() -> None:
     announce("fused attention B=1 (32 splits)")
     _case([5000], 4, 16, 8, 16, seed=13)
