@@ -1,9 +1,9 @@
-"""Multi-query causal paged attention: the drop-in for attention.paged_extend (oxr_runtime/attention.py:96-109).
+"""Multi-query causal paged attention: the drop-ins for attention.paged_extend (oxr_runtime/attention.py:96-109)
+and attention.paged_decode (attention.py:76-93).
 
 Runs the gfx950 kernels of csrc/paged_attention.hip (MFMA QK^T and PV tiles, context split
-across 8-wave workgroups merged on chip, then a small log-sum-exp merge of the splits).  Only the verify-step entry point is
-provided; the reference's prefill/vision/decode entry points (``varlen``,
-``varlen_bidirectional``, ``paged_decode``, ``rotary``) are outside this build.
+across 8-wave workgroups merged on chip, then a small log-sum-exp merge of the splits).  The reference's prefill and vision
+entry points (``varlen``, ``varlen_bidirectional``, ``rotary``) are outside this build.
 """
 
 from __future__ import annotations
@@ -59,6 +59,25 @@ def paged_extend(
         _lib.stream(device),
     )
     return out
+
+
+def paged_decode(
+    q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
+    block_table: torch.Tensor, *, scale: float | None = None, max_seq_len: int | None = None,
+    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The drop-in for attention.paged_decode (oxr_runtime/attention.py:76-93): one new token per
+    sequence (``q`` is ``[B, heads, dim]``, its K/V already in the paged cache; ``seq_lens`` includes
+    it) attending to every key of its sequence.  Returns ``[B, heads, dim]``.  The same kernels as
+    :func:`paged_extend` with one token per sequence."""
+    _lib.require(q.dim() == 3, "q must be [B, H, D]")
+    b, h, d = q.shape
+    if out is not None:
+        _lib.require(out.shape == q.shape and out.is_contiguous(), "out must be contiguous [B, H, D]")
+        out = out.view(b, 1, h, d)
+    res = paged_extend(q.view(b, 1, h, d), k_cache, v_cache, seq_lens, block_table, scale=scale,
+                       max_seq_len=max_seq_len, out=out, workspace=workspace)
+    return res.view(b, h, d)
 
 
 def qk_norm_rope_paged_extend(

@@ -1,7 +1,9 @@
 """HIP-graph capture and replay of the speculative verify step.
 
-Two entry points:
+Three entry points:
 
+- :class:`DecodeGraphs` is the one-token decode step (oxr_runtime/decode_graph.py:33-119): host lists
+  in, ``(logits, greedy ids)`` out, one graph per batch bucket, padded rows on a scratch page.
 - :class:`ExtendGraphs` keeps the reference's interface (oxr_runtime/decode_graph.py:122-205):
   host lists in, greedy ids ``[n, S]`` out, one graph per batch bucket (1, 2, 4, 8, max).
   Padded rows of a bucket write the first S slots of a scratch page and attend only to
@@ -21,10 +23,11 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from . import speculative
+from . import lm_head, speculative
 from .kv_cache import KVCache, pack_page_table
-from .language import ExtendBatch, LanguageModel, StepBuffers
+from .language import DecodeBatch, ExtendBatch, LanguageModel, StepBuffers
 
+BUCKETS = (1, 2, 4, 8, 16, 32, 64)  # decode_graph.py:30, up to what the weight-streaming kernels take
 EXTEND_BUCKETS = (1, 2, 4, 8)  # decode_graph.py:122
 
 
@@ -34,6 +37,89 @@ def _warm_up(stream: torch.cuda.Stream, forward, times: int = 2) -> None:
         for _ in range(times):
             forward()
     torch.cuda.current_stream().wait_stream(stream)
+
+
+class DecodeGraphs:
+    """The decode step for each batch bucket (decode_graph.py:33-119): :meth:`run` replays the
+    smallest bucket that holds the batch and returns None above the largest.  Padded rows write
+    and read only the first slot of a scratch page taken from ``cache`` (decode_graph.py:49-53).
+    The reference records buckets up to 1024 sequences; this build's GEMMs stream weights for at
+    most 64 token rows per launch, so ``max_batch`` is at most 64."""
+
+    def __init__(self, language: LanguageModel, cache: KVCache, *, max_batch: int, max_positions: int,
+                 stream: torch.cuda.Stream | None = None):
+        if not 1 <= max_batch <= BUCKETS[-1]:
+            raise ValueError(f"DecodeGraphs: max_batch must be in [1, {BUCKETS[-1]}]")
+        self.language = language
+        self.cache = cache
+        self.stream = stream or torch.cuda.Stream()
+        device = language.weights.lm_head.device
+        scratch = cache.allocate(1)
+        if scratch is None:
+            raise RuntimeError("DecodeGraphs: no free KV page for the scratch page")
+        bs = cache.block_size
+        self.scratch_block = scratch[0]
+        self.scratch_slot = self.scratch_block * bs
+        self.buckets = [b for b in BUCKETS if b < max_batch] + [max_batch]
+        self.width = -(-max_positions // bs)
+        top = self.buckets[-1]
+
+        self.ids = torch.zeros(top, dtype=torch.long, device=device)
+        self.positions = torch.zeros(top, dtype=torch.long, device=device)
+        self.slots = torch.full((top,), self.scratch_slot, dtype=torch.long, device=device)
+        self.seq_lens = torch.ones(top, dtype=torch.int32, device=device)
+        self.table = torch.full((top, self.width), self.scratch_block, dtype=torch.int32, device=device)
+        self._staging = [(dst, torch.empty_like(dst, device="cpu").pin_memory())
+                         for dst in (self.ids, self.positions, self.slots, self.seq_lens, self.table)]
+        self._host = [host.numpy() for _, host in self._staging]
+        self.buffers = StepBuffers.allocate(language.config, top, 1, self.width * bs, device)
+        self.logits = torch.empty(top, language.config.vocab_size, dtype=torch.bfloat16, device=device)
+
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        pool = torch.cuda.graph_pool_handle()
+        for bucket in reversed(self.buckets):
+            self._graphs[bucket] = self._capture(bucket, pool)
+
+    def _forward(self, bucket: int) -> tuple[torch.Tensor, torch.Tensor]:
+        batch = DecodeBatch(self.ids[:bucket], self.positions[:bucket], self.slots[:bucket], self.seq_lens[:bucket],
+                            self.table[:bucket])
+        hidden = self.language.decode(batch, self.cache, self.buffers)
+        tokens, logits = lm_head.lm_head_argmax(hidden, self.language.weights.lm_head,
+                                                predicted=self.buffers.predicted[:bucket],
+                                                logits=self.logits[:bucket], return_logits=True,
+                                                workspace=self.buffers.head_workspace)
+        return logits, tokens
+
+    def _capture(self, bucket: int, pool) -> tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]:
+        _warm_up(self.stream, lambda: self._forward(bucket))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=pool, stream=self.stream):
+            logits, tokens = self._forward(bucket)
+        return graph, logits, tokens
+
+    def run(self, ids: list[int], positions: list[int], slots: list[int], seq_lens: list[int],
+            tables: list[list[int]]) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """Replays one step; returns ``[n, vocab]`` bf16 logits and ``[n]`` greedy ids (views of the
+        bucket's outputs, valid until the next replay), or None when ``n`` exceeds the largest bucket."""
+        n = len(ids)
+        bucket = next((b for b in self.buckets if b >= n), None)
+        if bucket is None:
+            return None
+        h_ids, h_positions, h_slots, h_seq_lens, h_table = self._host
+        h_ids[:n] = ids
+        h_ids[n:bucket] = 0
+        h_positions[:n] = positions
+        h_positions[n:bucket] = 0
+        h_slots[:n] = slots
+        h_slots[n:bucket] = self.scratch_slot
+        h_seq_lens[:n] = seq_lens
+        h_seq_lens[n:bucket] = 1
+        pack_page_table(h_table[:bucket], tables, self.scratch_block)
+        for dst, host in self._staging:
+            dst[:bucket].copy_(host[:bucket], non_blocking=True)
+        graph, logits, tokens = self._graphs[bucket]
+        graph.replay()
+        return logits[:n], tokens[:n]
 
 
 class ExtendGraphs:

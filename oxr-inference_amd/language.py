@@ -157,6 +157,22 @@ class ExtendBatch:
 
 
 @dataclass
+class DecodeBatch:
+    """One decode step: one new token per sequence (language.py:54-66).  As with
+    :class:`ExtendBatch`, token ``ids`` replace the reference's ``embeds`` (which may still be given)."""
+
+    ids: torch.Tensor | None  # int64 [B]
+    positions: torch.Tensor   # int64 [B]
+    slots: torch.Tensor       # int64 [B]
+    seq_lens: torch.Tensor    # int32 [B], including the new token
+    block_table: torch.Tensor  # int32 [B, max_blocks]
+    embeds: torch.Tensor | None = None  # bf16 [B, hidden]
+
+    def as_extend(self) -> ExtendBatch:
+        return ExtendBatch(self.ids, self.positions, self.slots, self.seq_lens, self.block_table, 1, self.embeds)
+
+
+@dataclass
 class StepBuffers:
     """Every intermediate of one forward, allocated once for up to ``max_tokens`` rows."""
 
@@ -215,6 +231,12 @@ class LanguageModel:
         self.embed(batch, buffers)
         self.run_layers(batch, cache, buffers, 0, self.config.num_layers, first_norm_done=True)
         return self.final_norm(batch, buffers)
+
+    def decode(self, batch: DecodeBatch, cache: KVCache, buffers: StepBuffers | None = None) -> torch.Tensor:
+        """``[B, hidden]``: the final-norm hidden state of each sequence's new token (language.py:190-199).
+        The verify forward with one token per sequence: the same kernels, attention as
+        ``paged_decode``."""
+        return self.extend(batch.as_extend(), cache, buffers)
 
     def _buffers(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers | None) -> StepBuffers:
         _lib.require_gpu(batch.positions, batch.slots, batch.seq_lens, batch.block_table, name="extend")
