@@ -134,6 +134,38 @@ COPY_BYTES = 256 << 20  # calibration copy for the FETCH_SIZE / WRITE_SIZE count
 TRAFFIC_FILE = ROOT / "profiles" / "paged_extend_traffic.md"
 
 
+def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
+    """The one-token decode step (``DecodeGraphs``, decode_graph.py:33-119) for the same B sequences
+    at their current context: one new token each, graph replays with the inputs already on the
+    device.  Bytes = weights + LM head + every visible key's K/V once + the new K/V rows."""
+    b, bs = loop.batch, cache.block_size
+    width = loop.block_table.shape[1]
+    graphs = decode_graph.DecodeGraphs(model, cache, max_batch=b, max_positions=width * bs)
+    seq = loop.seq_len.cpu().numpy().astype(np.int64)
+    table = loop.block_table.cpu().numpy()
+    positions = seq.tolist()
+    slots = [int(table[i, p // bs]) * bs + p % bs for i, p in enumerate(positions)]
+    tables = [table[i, : (p + 1 + bs - 1) // bs].tolist() for i, p in enumerate(positions)]
+    graphs.run([1] * b, positions, slots, (seq + 1).tolist(), tables)
+    graph = graphs._graphs[graphs.buckets[-1]][0]
+    for _ in range(3):
+        graph.replay()
+    stream = torch.cuda.current_stream()  # where replay() launches the graph
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / iters
+    c = config
+    kv = float((seq + 1).sum()) * 2 * c.num_kv_heads * c.head_dim * 2 * c.num_layers
+    traffic = step_bytes(c, b, 1, 0.0)["weights"] + kv + b * 2 * c.num_kv_heads * c.head_dim * 2 * c.num_layers
+    return {"batch": b, "context": float(seq.mean()), "step_us": us, "bytes": traffic,
+            "achieved_gbs": traffic / (us * 1e-6) / 1e9}
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per attention launch from the committed rocprofv3 --pmc summary (FETCH_SIZE +
     WRITE_SIZE of both kernels, each scaled by the counter's reading for a copy of known size)."""
@@ -268,6 +300,8 @@ def main() -> int:
     attn = time_attention(config, model, cache, loop)
     attn_gbs = attn["bytes"] / (attn["us"] * 1e-6) / 1e9
     log(f"attention kernel {attn['us']:.2f} us, {attn_gbs:.0f} GB/s")
+    decode = time_decode(config, model, cache, loop)
+    log(f"decode step (B={decode['batch']}, one token each) {decode['step_us']:.1f} us")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -305,6 +339,9 @@ def main() -> int:
                      "bound": "hbm", "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": attn_gbs / HBM_PEAK_GBS, "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"],
                      "traffic": measured_traffic()},
+        "decode_step": {"batch": decode["batch"], "context": decode["context"], "us": decode["step_us"],
+                        "achieved": decode["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": decode["achieved_gbs"] / HBM_PEAK_GBS},
         "cpu_baseline": cpu,
         "wall_s_timed": wall,
     }
