@@ -261,6 +261,20 @@ int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight
                        oxr_stream_t stream);
 
 /*
+ * (3c) Variable-length (prefill) attention.  Replaces attention.varlen
+ * (oxr_runtime/attention.py:47-59): sequences concatenated along the token
+ * axis, q bf16 [T, num_heads, 128], k and v bf16 [T, num_kv_heads, 128],
+ * cu_seqlens int32 [num_seqs + 1] (sequence i is tokens [cu[i], cu[i+1]),
+ * every length <= max_len).  Within each sequence, query token j of head h
+ * attends keys [0, j] when causal != 0, else all keys, of kv head
+ * h / (num_heads / num_kv_heads); scores q.k * scale, fp32 softmax, output
+ * bf16 [T, num_heads, 128].  num_heads / num_kv_heads must be 1, 2, 4 or 8.
+ */
+int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const oxr_bf16* v, const int32_t* cu_seqlens,
+                         int32_t num_seqs, int32_t max_len, int32_t num_heads, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t causal, float scale, oxr_bf16* out, oxr_stream_t stream);
+
+/*
  * (4c) Packed weights and token rows.  The reference keeps nn.Linear weights row-major
  * ([rows, k], language.py:234-245 and the LM head of :213-214); these entry
  * points take the same weights re-ordered once, at load time, into the order

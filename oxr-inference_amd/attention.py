@@ -1,9 +1,10 @@
-"""Multi-query causal paged attention: the drop-ins for attention.paged_extend (oxr_runtime/attention.py:96-109)
-and attention.paged_decode (attention.py:76-93).
+"""Attention on gfx950: the drop-ins for attention.paged_extend (oxr_runtime/attention.py:96-109),
+attention.paged_decode (attention.py:76-93) and attention.varlen (attention.py:47-59).
 
-Runs the gfx950 kernels of csrc/paged_attention.hip (MFMA QK^T and PV tiles, context split
-across 8-wave workgroups merged on chip, then a small log-sum-exp merge of the splits).  The reference's prefill and vision
-entry points (``varlen``, ``varlen_bidirectional``, ``rotary``) are outside this build.
+The paged entry points run csrc/paged_attention.hip (MFMA QK^T and PV tiles, context split across
+8-wave workgroups merged on chip, then a small log-sum-exp merge of the splits); ``varlen`` runs
+csrc/varlen_attention.hip (key tiles staged in LDS and shared by 128 query rows).  The vision
+entry points (``varlen_bidirectional`` with head dim 72, ``rotary``) are outside this build.
 """
 
 from __future__ import annotations
@@ -58,6 +59,33 @@ def paged_extend(
         float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         _lib.stream(device),
     )
+    return out
+
+
+def varlen(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor, max_len: int, *, causal: bool,
+    scale: float | None = None, out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The drop-in for attention.varlen (oxr_runtime/attention.py:47-59): sequences concatenated along
+    the token axis (``q`` ``[T, heads, 128]``, ``k``/``v`` ``[T, kv_heads, 128]``, ``cu_seqlens`` int32
+    ``[n + 1]``), attention within each sequence, causal or not.  Returns ``[T, heads, 128]``."""
+    device = _lib.require_gpu(q, k, v, cu_seqlens, name="varlen")
+    _lib.require(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+                 "varlen: bf16 q, k, v required")
+    _lib.require(q.dim() == 3 and k.dim() == 3 and k.shape == v.shape and q.shape[0] == k.shape[0]
+                 and q.shape[2] == k.shape[2], "varlen: q [T, H, D], k and v [T, KV, D]")
+    _lib.require(q.is_contiguous() and k.is_contiguous() and v.is_contiguous(), "varlen: contiguous q, k, v")
+    _lib.require(cu_seqlens.dtype == torch.int32 and cu_seqlens.dim() == 1 and cu_seqlens.is_contiguous(),
+                 "varlen: cu_seqlens must be contiguous int32 [n + 1]")
+    t, h, d = q.shape
+    if scale is None:
+        scale = d ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    _lib.require(out.shape == q.shape and out.dtype == torch.bfloat16 and out.is_contiguous(), "varlen: out like q")
+    _lib.call("oxr_varlen_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens.data_ptr(),
+              cu_seqlens.shape[0] - 1, int(max_len), h, k.shape[1], d, 1 if causal else 0, float(scale),
+              out.data_ptr(), _lib.stream(device))
     return out
 
 

@@ -1,0 +1,66 @@
+"""gfx950 variable-length (prefill) attention vs the oracle (bf16 tolerance: |err| <= 2e-2 + 1e-2 |ref|).
+
+``attention.varlen`` is the drop-in for attention.varlen (oxr_runtime/attention.py:47-59).  Cases:
+lengths around the 16-row query and 64-key tile edges, an empty sequence, one-token sequences,
+causal and bidirectional, every supported head grouping (1, 2, 4 and 8 q heads per kv head),
+and prefill-sized sequences.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, pkg
+from oracle import attention as oracle_attention
+
+pytestmark = pytest.mark.gpu
+attention = pkg("attention")
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _case(lens, H, KV, causal, seed):
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(T, H, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(T, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(T, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.full_like(q, float("nan"))
+    announce("varlen", lens if len(lens) < 12 else f"{len(lens)} seqs", H, KV, "causal" if causal else "bidir")
+    attention.varlen(q, k, v, torch.from_numpy(cu).cuda(), max(lens), causal=causal, out=out)
+    torch.cuda.synchronize()
+    exact = oracle_attention.varlen(_bits(q), _bits(k), _bits(v), cu, 128 ** -0.5, causal)
+    got = out.float().cpu().numpy()
+    err = np.abs(got - exact)
+    bound = ATOL + RTOL * np.abs(exact)
+    assert np.isfinite(got).all(), "rows left unwritten"
+    assert (err <= bound).all(), f"max err {err.max():.3g}, worst excess {(err - bound).max():.3g}"
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_tile_edges_and_empty(causal) -> None:
+    _case([1, 15, 16, 17, 0, 63, 64, 65, 127, 128, 129, 200], 16, 8, causal, seed=1 + causal)
+
+
+@pytest.mark.parametrize("kv", [16, 8, 4, 2])
+def test_head_groupings(kv) -> None:
+    _case([97, 300, 1], 16, kv, True, seed=10 + kv)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_sizes(causal) -> None:
+    _case([1024, 777], 16, 8, causal, seed=20 + causal)
+
+
+def test_rejects_unsupported_grouping() -> None:
+    q = torch.zeros(4, 12, 128, dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros(4, 4, 128, dtype=torch.bfloat16, device="cuda")  # 3 q heads per kv head
+    with pytest.raises(RuntimeError):
+        attention.varlen(q, k, k, torch.tensor([0, 4], dtype=torch.int32, device="cuda"), 4, causal=True)
