@@ -12,16 +12,17 @@
 // every query row of the workgroup:
 // * A workgroup is 8 waves covering 128 query rows: the G = H / KV q heads of
 //   one kv head, 128 / G consecutive positions each (16 rows per wave).
-// * Key tiles of 64 rows are loaded cooperatively (one 16-byte piece of K and
-//   of V per thread and tile half), written to LDS -- K row-major with a 16-
-//   byte row pad (conflict-free fragment reads), V transposed to [dim][key]
-//   (the PV product needs 8 keys of one dim per lane) -- double-buffered: tile
-//   t + 1 is in registers while tile t is multiplied.
+// * Key tiles of 64 rows are loaded cooperatively (two 16-byte pieces of K and
+//   of V per thread), written to LDS row-major with 16-byte stores and a
+//   32-byte row pad (rows 72 dwords apart: conflict-free fragment reads),
+//   double-buffered: tile t + 1 is in registers while tile t is multiplied.
+//   The PV product needs 8 keys of one dim per lane; gfx950's transposing LDS
+//   read (ds_read_b64_tr_b16) gathers them from the row-major V tile.
 // * Per wave and tile: S^T = K Q^T (16 MFMAs 16x16x32: 4 key blocks x 4 dim
 //   steps; lane (r, g) holds keys 4g..4g+3 of each key block for query r), an
 //   exp2-domain online softmax, then O^T += V^T P^T (16 MFMAs; P^T is used as
 //   computed: key slot 8g + 4p + j of a 32-key step stands for key 16p + 4g + j,
-//   and the V^T fragments are read from LDS in the same order).
+//   and the V^T fragments are gathered in the same order).
 // * Causal: key tiles above a wave's last row are skipped, the diagonal tile
 //   is masked per element; keys past the sequence are masked.
 #include "common.h"
@@ -33,15 +34,25 @@ constexpr int kVD = 128;           // head dim
 constexpr int kVWaves = 8;         // waves per workgroup
 constexpr int kVRows = 16 * kVWaves;  // query rows per workgroup (all q heads of the kv head)
 constexpr int kKeyTile = 64;       // keys per LDS stage
-constexpr int kKPitch = kVD + 8;   // bf16 per K row in LDS (16-byte pad)
-constexpr int kVPitch = kKeyTile + 8;  // bf16 per V^T row in LDS
+constexpr int kKPitch = kVD + 16;  // bf16 per K row in LDS (32-byte pad: conflict-free fragment reads)
+constexpr int kVPitch = kVD + 16;  // bf16 per V row in LDS (32-byte pad: conflict-free transposing reads)
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b16).  Within each group of 16 lanes,
+// lane 4a + b receives element b of the 4 bf16 addressed by lanes a, a + 4,
+// a + 8 and a + 12 of its group, in that order.
+__device__ __forceinline__ u32x2 lds_read_tr16(const bf16_t* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (v4s __attribute__((address_space(3)))*)(const_cast<bf16_t*>(p)));
+  return __builtin_bit_cast(u32x2, x);
+}
 
 template <bool kCausal>
 __global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ cu_seqlens, int H, int KV, float scale_log2, bf16_t* __restrict__ out) {
   __shared__ bf16_t s_k[2][kKeyTile][kKPitch];
-  __shared__ bf16_t s_vt[2][kVD][kVPitch];
+  __shared__ bf16_t s_v[2][kKeyTile][kVPitch];
 
   const int seq = blockIdx.z, kvh = blockIdx.y;
   const int start = cu_seqlens[seq], len = cu_seqlens[seq + 1] - start;
@@ -73,30 +84,26 @@ __global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
   const int wave_last = kCausal ? min(w0 + 15, len - 1) : len - 1;
   const int tiles = (key_end + kKeyTile - 1) / kKeyTile;
 
-  // Cooperative staging: thread t loads dims [16 (t / 64), +16) of key
-  // (t % 64) of the tile from K and from V, as two 16-byte pieces each; keys
-  // past the sequence re-read its last key (their scores are masked).
-  const int st_key = tid & 63, st_d = (tid >> 6) * 16;
+  // Cooperative staging: 16-byte piece p = t + 512h (h = 0, 1) of the tile is
+  // dims [8 (p % 16), +8) of key p / 16, from K and from V (a wave covers 4
+  // whole rows); keys past the sequence re-read its last key (their scores are
+  // masked).  Both are stored row-major.
+  const int st_key = tid >> 4, st_d = (tid & 15) * 8;
   u32x4 kr[2], vr[2];
   auto fetch = [&](int t) {
-    const int key = min(t * kKeyTile + st_key, len - 1);
-    const int64_t row = ((int64_t)(start + key) * KV + kvh) * kVD + st_d;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      kr[h] = ld128(k + row + 8 * h);
-      vr[h] = ld128(v + row + 8 * h);
+      const int key = min(t * kKeyTile + st_key + 32 * h, len - 1);
+      const int64_t row = ((int64_t)(start + key) * KV + kvh) * kVD + st_d;
+      kr[h] = ld128(k + row);
+      vr[h] = ld128(v + row);
     }
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) *reinterpret_cast<u32x4*>(&s_k[buf][st_key][st_d + 8 * h]) = kr[h];
-    // V transposed: 16 dims of one key into 16 rows of V^T.
-#pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t w[4] = {vr[h].x, vr[h].y, vr[h].z, vr[h].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        s_vt[buf][st_d + 8 * h + e][st_key] = (bf16_t)((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      *reinterpret_cast<u32x4*>(&s_k[buf][st_key + 32 * h][st_d]) = kr[h];
+      *reinterpret_cast<u32x4*>(&s_v[buf][st_key + 32 * h][st_d]) = vr[h];
     }
   };
 
@@ -163,9 +170,12 @@ __global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
                           pack_bf_hw(pv[8 * s + 4], pv[8 * s + 5]), pack_bf_hw(pv[8 * s + 6], pv[8 * s + 7])};
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-          const bf16_t* vt = &s_vt[buf][16 * dt + r][32 * s + 4 * g];
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vt);       // keys 32s + 4g .. +3
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vt + 16);  // keys 32s + 16 + 4g .. +3
+          // A = V^T: lane (r, g) gets dim 16 dt + r of keys 32s + 16p + 4g + (0..3), p = 0, 1, from
+          // two transposing reads in which lane j of the group addresses key 32s + 16p + 4g + j / 4,
+          // dims 16 dt + 4 (j % 4) .. +3.
+          const bf16_t* vp = &s_v[buf][32 * s + 4 * g + (r >> 2)][16 * dt + 4 * (r & 3)];
+          const u32x2 lo = lds_read_tr16(vp);
+          const u32x2 hi = lds_read_tr16(vp + 16 * kVPitch);
           o[dt] = mfma_16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, o[dt]);
         }
       }
