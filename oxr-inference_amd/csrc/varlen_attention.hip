@@ -7,35 +7,46 @@
 // keys [0, j] (causal) or all keys (bidirectional) of kv head h / (H / KV);
 // scores q.k * scale, fp32 softmax, bf16 output [T, H, 128].
 //
-// Prefill attention is MFMA-bound (Θ(len²) work per sequence), so unlike the
-// verify kernel the keys are staged once per workgroup in LDS and shared by
-// every query row of the workgroup:
-// * A workgroup is 8 waves covering 128 query rows: the G = H / KV q heads of
-//   one kv head, 128 / G consecutive positions each (16 rows per wave).
-// * Key tiles of 64 rows are loaded cooperatively (two 16-byte pieces of K and
-//   of V per thread), written to LDS row-major with 16-byte stores and a
-//   32-byte row pad (rows 72 dwords apart: conflict-free fragment reads),
+// Prefill attention is MFMA-bound (Θ(len²) work per sequence), so the keys are
+// staged once per workgroup in LDS and shared by every query row of the
+// workgroup, and the products use the 32x32x16 MFMA, which reads half the LDS
+// bytes per flop of the 16x16x32 one (LDS read bandwidth is the next limit):
+// * A workgroup is 4 waves covering 128 query rows: the G = H / KV q heads of
+//   one kv head, 128 / G consecutive positions each; wave w owns rows
+//   32w .. 32w + 31 (one per MFMA column; row rho is head slot rho / (128 / G),
+//   position q0 + rho % (128 / G)).
+// * Key tiles of 64 rows are loaded cooperatively (four 16-byte pieces of K
+//   and of V per thread), written to LDS row-major with 16-byte stores,
 //   double-buffered: tile t + 1 is in registers while tile t is multiplied.
-//   The PV product needs 8 keys of one dim per lane; gfx950's transposing LDS
-//   read (ds_read_b64_tr_b16) gathers them from the row-major V tile.
-// * Per wave and tile: S^T = K Q^T (16 MFMAs 16x16x32: 4 key blocks x 4 dim
-//   steps; lane (r, g) holds keys 4g..4g+3 of each key block for query r), an
-//   exp2-domain online softmax, then O^T += V^T P^T (16 MFMAs; P^T is used as
-//   computed: key slot 8g + 4p + j of a 32-key step stands for key 16p + 4g + j,
-//   and the V^T fragments are gathered in the same order).
-// * Causal: key tiles above a wave's last row are skipped, the diagonal tile
-//   is masked per element; keys past the sequence are masked.
+//   Row pitches 68 dwords (K) and 80 dwords (V) make the fragment reads below
+//   free of bank conflicts (measured on gfx950 for exactly these patterns).
+// * Per wave and tile: S^T = K Q^T (16 MFMAs: 2 key blocks x 8 dim steps;
+//   lane (n, h) holds keys 32kb + 8(v/4) + 4h + v%4 for query n), an
+//   exp2-domain online softmax, then O^T += V^T P^T (16 MFMAs: 4 dim blocks x
+//   4 key steps; P^T is used as computed: k slot 8h + 4p + j of key step ks
+//   stands for key 16ks + 8p + 4h + j).  The V^T fragments come from gfx950's
+//   transposing LDS read (ds_read_b64_tr_b16) of the row-major V tile.
+// * Causal: key tiles above a wave's last row are skipped, tiles that cross a
+//   row's diagonal are masked per element; keys past the sequence are masked.
 #include "common.h"
 
 namespace oxr {
 namespace {
 
-constexpr int kVD = 128;           // head dim
-constexpr int kVWaves = 8;         // waves per workgroup
-constexpr int kVRows = 16 * kVWaves;  // query rows per workgroup (all q heads of the kv head)
-constexpr int kKeyTile = 64;       // keys per LDS stage
-constexpr int kKPitch = kVD + 16;  // bf16 per K row in LDS (32-byte pad: conflict-free fragment reads)
-constexpr int kVPitch = kVD + 16;  // bf16 per V row in LDS (32-byte pad: conflict-free transposing reads)
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kVD = 128;               // head dim
+constexpr int kVWaves = 4;             // waves per workgroup
+constexpr int kVRows = 32 * kVWaves;   // query rows per workgroup (all q heads of the kv head)
+constexpr int kKeyTile = 64;           // keys per LDS stage
+constexpr int kKPitch = kVD + 8;       // bf16 per K row in LDS (68 dwords)
+constexpr int kVPitch = kVD + 32;      // bf16 per V row in LDS (80 dwords)
+constexpr int kPieces = kKeyTile * kVD / 8 / (64 * kVWaves);  // 16-byte pieces of K (and of V) per thread
+
+__device__ __forceinline__ f32x16 mfma_32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16).  Within each group of 16 lanes,
 // lane 4a + b receives element b of the 4 bf16 addressed by lanes a, a + 4,
@@ -48,69 +59,89 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const bf16_t* p) {
 }
 
 template <bool kCausal>
-__global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
+__global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const int32_t* __restrict__ cu_seqlens, int H, int KV, float scale_log2, bf16_t* __restrict__ out) {
+    const int32_t* __restrict__ cu_seqlens, int H, int KV, int num_qtiles, float scale_log2,
+    bf16_t* __restrict__ out) {
   __shared__ bf16_t s_k[2][kKeyTile][kKPitch];
   __shared__ bf16_t s_v[2][kKeyTile][kVPitch];
 
-  const int seq = blockIdx.z, kvh = blockIdx.y;
+  // Workgroup b runs on XCD b % 8 (round-robin dispatch).  XCD x takes the x-th eighth of the
+  // work items, in order, so the query tiles resident on one XCD at a time belong to one or two
+  // (sequence, kv head) pairs and share that pair's key tiles in the XCD's L2.  Item w is query
+  // tile w % num_qtiles (late tiles first) of pair w / num_qtiles.
+  const int total = (int)gridDim.x, xcd = (int)blockIdx.x & 7, slot = (int)blockIdx.x >> 3;
+  const int w = xcd * (total >> 3) + min(xcd, total & 7) + slot;
+  const int pair = w / num_qtiles;
+  const int seq = pair / KV, kvh = pair - seq * KV;
   const int start = cu_seqlens[seq], len = cu_seqlens[seq + 1] - start;
-  const int G = H / KV, rows_per_head = kVRows / G;
+  const int G = H / KV, rph = kVRows / G;  // positions per head in this workgroup
   // Query tiles in reverse order: under the causal mask the late ones do the most work, so they
   // are dispatched first.
-  const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * rows_per_head;  // first position, per head
-  if (q0 >= len) return;                            // whole workgroup: before any barrier
+  const int q0 = (num_qtiles - 1 - (w - pair * num_qtiles)) * rph;  // first position, per head
+  if (q0 >= len) return;                                    // whole workgroup: before any barrier
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, g = lane >> 4;
-  const int waves_per_head = kVWaves / G;
-  const int head = kvh * G + wave / waves_per_head;
-  const int w0 = q0 + 16 * (wave % waves_per_head);  // this wave's first query position
-  const int qpos = w0 + r;                           // query position of lane row r
+  const int n = lane & 31, h = lane >> 5;
+  const int rho = 32 * wave + n;
+  const int head = kvh * G + rho / rph;
+  const int qpos = q0 + rho % rph;  // query position of lane column n
+  // The wave's positions: offsets first_off .. first_off + min(rph, 32) - 1 from q0.
+  const int first_off = rph >= 32 ? (32 * wave) % rph : 0;
+  const int wave_first = q0 + first_off;
+  const int wave_last = kCausal ? min(wave_first + min(rph, 32) - 1, len - 1) : len - 1;
 
-  // Q^T fragments (B operand): lane (r, g) holds Q[w0 + r][32i + 8g, +8) for dim step i.
-  u32x4 qf[4];
+  // Q^T fragments (B operand): lane (n, h) holds Q[qpos][16i + 8h, +8) for dim step i.
+  u32x4 qf[8];
   {
     const int qrow = min(qpos, len - 1);  // rows past the sequence compute and are never stored
-    const bf16_t* src = q + ((int64_t)(start + qrow) * H + head) * kVD + 8 * g;
+    const bf16_t* src = q + ((int64_t)(start + qrow) * H + head) * kVD + 8 * h;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qf[i] = ld128(src + 32 * i);
+    for (int i = 0; i < 8; ++i) qf[i] = ld128(src + 16 * i);
   }
+  // Q lands here: otherwise the compiler sinks these loads past the first barrier and then, unable
+  // to tell them from the key-tile prefetch, waits for every tile's prefetch before its first
+  // product.
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(qf[i]));
 
-  // Keys this workgroup needs, and the last key any of this wave's rows sees.
-  const int key_end = kCausal ? min(len, q0 + rows_per_head) : len;
-  const int wave_last = kCausal ? min(w0 + 15, len - 1) : len - 1;
+  const int key_end = kCausal ? min(len, q0 + rph) : len;  // keys this workgroup needs
   const int tiles = (key_end + kKeyTile - 1) / kKeyTile;
 
-  // Cooperative staging: 16-byte piece p = t + 512h (h = 0, 1) of the tile is
-  // dims [8 (p % 16), +8) of key p / 16, from K and from V (a wave covers 4
-  // whole rows); keys past the sequence re-read its last key (their scores are
-  // masked).  Both are stored row-major.
+  // Cooperative staging: 16-byte piece p = t + 256u (u < 4) of the tile is dims
+  // [8 (p % 16), +8) of key p / 16, from K and from V (a wave covers 4 whole
+  // rows); keys past the sequence re-read its last key (their scores are masked).
   const int st_key = tid >> 4, st_d = (tid & 15) * 8;
-  u32x4 kr[2], vr[2];
+  u32x4 kr[kPieces], vr[kPieces];
   auto fetch = [&](int t) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int key = min(t * kKeyTile + st_key + 32 * h, len - 1);
+    for (int u = 0; u < kPieces; ++u) {
+      const int key = min(t * kKeyTile + st_key + 16 * u, len - 1);
       const int64_t row = ((int64_t)(start + key) * KV + kvh) * kVD + st_d;
-      kr[h] = ld128(k + row);
-      vr[h] = ld128(v + row);
+      kr[u] = ld128(k + row);
+      vr[u] = ld128(v + row);
     }
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *reinterpret_cast<u32x4*>(&s_k[buf][st_key + 32 * h][st_d]) = kr[h];
-      *reinterpret_cast<u32x4*>(&s_v[buf][st_key + 32 * h][st_d]) = vr[h];
+    for (int u = 0; u < kPieces; ++u) {
+      *reinterpret_cast<u32x4*>(&s_k[buf][st_key + 16 * u][st_d]) = kr[u];
+      *reinterpret_cast<u32x4*>(&s_v[buf][st_key + 16 * u][st_d]) = vr[u];
     }
   };
 
   float m_run = -INFINITY, mc_run = 0.f, l_run = 0.f;
-  f32x4 o[8];
+  f32x16 o[4];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+
+  // Transposing-read address of lane (n, h) for V^T fragment (dim block dt, key step ks, half p):
+  // lane j of its 16-lane group addresses key 16ks + 8p + 4h + j / 4, dims 32dt + 16 (n / 16) + 4 (j % 4).
+  const int tr_key = 4 * h + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   fetch(0);
   stash(0);
@@ -120,32 +151,40 @@ __global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
     if (t + 1 < tiles) fetch(t + 1);  // in flight during this tile's products
     const int kt0 = t * kKeyTile;
     if (kt0 <= wave_last) {  // wave-uniform: otherwise every key of the tile is masked for this wave
-      // Raw scores of keys kt0 + 16kb + 4g + j for query row r.
-      float sv[16];
+      // Raw scores: sv[kb][v] is key kt0 + 32kb + 8(v/4) + 4h + v%4 for query n.
+      // The two key blocks' chains alternate, so consecutive products are independent.
+      f32x16 sv[2];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(&s_k[buf][16 * kb + r][32 * i + 8 * g]);
-          acc = mfma_16x16x32(kf, qf[i], acc);
+        for (int e = 0; e < 16; ++e) sv[kb][e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(&s_k[buf][32 * kb + n][16 * i + 8 * h]);
+          sv[kb] = mfma_32x32x16(kf, qf[i], sv[kb]);
         }
+      // wave-uniform: a tile crossing the diagonal of one of the wave's rows, or the sequence end
+      const bool edge = (kCausal && kt0 + kKeyTile - 1 > wave_first) || kt0 + kKeyTile > len;
+      if (edge) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sv[4 * kb + j] = acc[j];
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = kt0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (key >= len || (kCausal && key > qpos)) sv[kb][e] = -INFINITY;
+          }
       }
-      const bool edge = kt0 + kKeyTile - 1 > (kCausal ? w0 : len - 1) || kt0 + kKeyTile > len;
-      if (edge) {  // wave-uniform: the diagonal tile or the sequence's last tile
+      // Row maximum as a tree (max is exact in any order).
+      float mt[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kt0 + 16 * (e >> 2) + 4 * g + (e & 3);
-          if (key >= len || (kCausal && key > qpos)) sv[e] = -INFINITY;
-        }
-      }
-      float mx = sv[0];
+      for (int e = 0; e < 16; ++e) mt[e] = fmaxf(sv[0][e], sv[1][e]);
 #pragma unroll
-      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sv[e]);
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+      for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int e = 0; e < w; ++e) mt[e] = fmaxf(mt[e], mt[e + w]);
+      const float mx = fmaxf(mt[0], shfl_xor_f(mt[0], 32));
       const bool moved = mx > m_run;
       if (__builtin_amdgcn_ballot_w64(moved)) {
         const float m_new = moved ? mx : m_run;
@@ -153,30 +192,38 @@ __global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
         const float alpha = !moved ? 1.0f : (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc_run - mc_new));
         l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
         m_run = m_new;
         mc_run = mc_new;
       }
-      float pv[16];
+      // P^T for key step ks: accumulators 8 (ks % 2) .. +7 of key block ks / 2, in k-slot order.
+      // The tile's probabilities are summed as a tree, then added to the running sum.
+      u32x4 pb[4];
+      float ps[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], scale_log2, -mc_run));
-        l_run += pv[e];
+      for (int ks = 0; ks < 4; ++ks) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[ks >> 1][8 * (ks & 1) + e], scale_log2, -mc_run));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ps[4 * ks + e] = pv[e] + pv[e + 4];
+        pb[ks] = u32x4{pack_bf_hw(pv[0], pv[1]), pack_bf_hw(pv[2], pv[3]), pack_bf_hw(pv[4], pv[5]),
+                       pack_bf_hw(pv[6], pv[7])};
       }
-      // Two 32-key steps; P^T slot 8g + 4p + j is key 16 (2s + p) + 4g + j.
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 pb = {pack_bf_hw(pv[8 * s + 0], pv[8 * s + 1]), pack_bf_hw(pv[8 * s + 2], pv[8 * s + 3]),
-                          pack_bf_hw(pv[8 * s + 4], pv[8 * s + 5]), pack_bf_hw(pv[8 * s + 6], pv[8 * s + 7])};
+      for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          // A = V^T: lane (r, g) gets dim 16 dt + r of keys 32s + 16p + 4g + (0..3), p = 0, 1, from
-          // two transposing reads in which lane j of the group addresses key 32s + 16p + 4g + j / 4,
-          // dims 16 dt + 4 (j % 4) .. +3.
-          const bf16_t* vp = &s_v[buf][32 * s + 4 * g + (r >> 2)][16 * dt + 4 * (r & 3)];
-          const u32x2 lo = lds_read_tr16(vp);
-          const u32x2 hi = lds_read_tr16(vp + 16 * kVPitch);
-          o[dt] = mfma_16x16x32(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, o[dt]);
+        for (int e = 0; e < w; ++e) ps[e] += ps[e + w];
+      l_run += ps[0];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16_t* vp = &s_v[buf][16 * ks + tr_key][tr_dim];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const u32x2 lo = lds_read_tr16(vp + 32 * dt);                // keys 16ks + 4h + (0..3)
+          const u32x2 hi = lds_read_tr16(vp + 8 * kVPitch + 32 * dt);  // keys 16ks + 8 + 4h + (0..3)
+          o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[ks], o[dt]);
         }
       }
     }
@@ -184,16 +231,18 @@ __global__ __launch_bounds__(64 * kVWaves) void varlen_attention_kernel(
     __syncthreads();
   }
 
-  // Normalise and store: lane (r, g) holds O^T[16 dt + 4g + j][query r].
-  float l_tot = l_run + shfl_xor_f(l_run, 16);
-  l_tot += shfl_xor_f(l_tot, 32);
+  // Normalise and store: lane (n, h) holds O^T[32dt + 8(e/4) + 4h + e%4][query n].
+  float l_tot = l_run + shfl_xor_f(l_run, 32);
   if (qpos < len) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    bf16_t* dst = out + ((int64_t)(start + qpos) * H + head) * kVD + 4 * g;
+    bf16_t* dst = out + ((int64_t)(start + qpos) * H + head) * kVD + 4 * h;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      *reinterpret_cast<u32x2*>(dst + 16 * dt) =
-          u32x2{pack_bf(o[dt][0] * inv, o[dt][1] * inv), pack_bf(o[dt][2] * inv, o[dt][3] * inv)};
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * m) =
+            u32x2{pack_bf(o[dt][4 * m] * inv, o[dt][4 * m + 1] * inv),
+                  pack_bf(o[dt][4 * m + 2] * inv, o[dt][4 * m + 3] * inv)};
   }
 }
 
@@ -208,22 +257,22 @@ extern "C" int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const 
   OXR_RETURN_IF(num_seqs < 0 || max_len < 0 || num_heads <= 0 || num_kv_heads <= 0, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(head_dim != kVD || num_heads % num_kv_heads != 0, OXR_ERR_UNSUPPORTED);
   const int G = num_heads / num_kv_heads;
-  OXR_RETURN_IF(kVWaves % G != 0, OXR_ERR_UNSUPPORTED);  // G in {1, 2, 4, 8}
-  OXR_RETURN_IF(num_seqs > 65535 || num_kv_heads > 65535, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(8 % G != 0, OXR_ERR_UNSUPPORTED);  // G in {1, 2, 4, 8}
   if (num_seqs == 0 || max_len == 0) return OXR_OK;
   OXR_RETURN_IF(!q || !k || !v || !cu_seqlens || !out, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 != 0 || (uintptr_t)out % 8 != 0,
                 OXR_ERR_UNSUPPORTED);
   const int rows_per_head = kVRows / G;
-  const dim3 grid((unsigned)((max_len + rows_per_head - 1) / rows_per_head), (unsigned)num_kv_heads,
-                  (unsigned)num_seqs);
+  const int num_qtiles = (max_len + rows_per_head - 1) / rows_per_head;
+  OXR_RETURN_IF((int64_t)num_qtiles * num_kv_heads * num_seqs > INT32_MAX, OXR_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)(num_qtiles * num_kv_heads * num_seqs));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   if (causal)
     hipLaunchKernelGGL(varlen_attention_kernel<true>, grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
-                       num_heads, num_kv_heads, scale_log2, out);
+                       num_heads, num_kv_heads, num_qtiles, scale_log2, out);
   else
     hipLaunchKernelGGL(varlen_attention_kernel<false>, grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
-                       num_heads, num_kv_heads, scale_log2, out);
+                       num_heads, num_kv_heads, num_qtiles, scale_log2, out);
   return OXR_LAUNCH_STATUS();
 }
