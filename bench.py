@@ -43,6 +43,7 @@ workloads = importlib.import_module(f"{PKG}.workloads")
 
 METRIC = "accepted tokens/sec + verify-step latency (us) at B=8,k=3; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
 def log(*parts) -> None:
@@ -166,6 +167,37 @@ def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
             "achieved_gbs": traffic / (us * 1e-6) / 1e9}
 
 
+def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, seed: int = 0) -> dict:
+    """Prefill attention (``attention.varlen``, the drop-in for attention.py:47-59): causal over
+    ``seqs`` sequences of ``length`` tokens at the model's head shape, inputs resident on the device.
+    Flops = 4 * head_dim * heads * (causal query-key pairs)."""
+    h, kv, d = config.num_heads, config.num_kv_heads, config.head_dim
+    t = seqs * length
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(t, h, d, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(t, kv, d, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(t, kv, d, generator=g, device="cuda").to(torch.bfloat16)
+    cu = torch.arange(0, t + 1, length, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    for _ in range(3):
+        attention.varlen(q, k, v, cu, length, causal=True, out=out)
+    stream = torch.cuda.current_stream()  # where the wrapper launches
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        attention.varlen(q, k, v, cu, length, causal=True, out=out)
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / iters
+    flops = 4.0 * d * h * seqs * (length * (length + 1) / 2)
+    tflops = flops / (us * 1e-6) / 1e12
+    del q, k, v, out
+    return {"workload": f"varlen causal, {seqs} x {length} tokens, {h}/{kv} heads, head_dim {d}", "us": us,
+            "flops": flops, "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per attention launch from the committed rocprofv3 --pmc summary (FETCH_SIZE +
     WRITE_SIZE of both kernels, each scaled by the counter's reading for a copy of known size)."""
@@ -250,6 +282,7 @@ def main() -> int:
     p.add_argument("--cpu-steps", type=int, default=12)
     p.add_argument("--pmc-driver", action="store_true", help="only attention launches + a calibration copy")
     p.add_argument("--cpu-warmup", type=int, default=1)
+    p.add_argument("--prefill-driver", action="store_true", help="only the prefill attention measurement")
     args = p.parse_args()
 
     if args.gpus != 1:
@@ -262,6 +295,9 @@ def main() -> int:
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
 
+    if args.prefill_driver:
+        print(json.dumps(time_prefill(language.QWEN_SYNTHETIC)), flush=True)
+        return 0
     log("building workload")
     config, model, cache, table, histories, seq_lens, width = build_workload(args, device)
     loop = decode_graph.VerifyLoop(model, cache, batch=args.batch, k=args.k, max_n=args.max_n,
@@ -302,6 +338,8 @@ def main() -> int:
     log(f"attention kernel {attn['us']:.2f} us, {attn_gbs:.0f} GB/s")
     decode = time_decode(config, model, cache, loop)
     log(f"decode step (B={decode['batch']}, one token each) {decode['step_us']:.1f} us")
+    prefill = time_prefill(config)
+    log(f"prefill attention {prefill['us']:.1f} us, {prefill['achieved']:.0f} TFLOP/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -342,6 +380,7 @@ def main() -> int:
         "decode_step": {"batch": decode["batch"], "context": decode["context"], "us": decode["step_us"],
                         "achieved": decode["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": decode["achieved_gbs"] / HBM_PEAK_GBS},
+        "prefill_attention": prefill,
         "cpu_baseline": cpu,
         "wall_s_timed": wall,
     }
