@@ -177,7 +177,9 @@ int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t r
  * are clamped to it.  workspace: at least
  * oxr_paged_extend_workspace_bytes(batch, KV, max_seq_len) bytes of device
  * memory for the context split's partials (no initial contents needed; calls
- * that overlap in time must not share a workspace).
+ * that overlap in time must not share a workspace).  A workspace sized for a
+ * batch serves every smaller batch (smaller batches split their contexts
+ * further; the size is the largest need up to `batch`).
  */
 size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
 int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache, const int32_t* seq_lens,

@@ -519,10 +519,14 @@ int pick_hpw(int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads) {
 extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
   using namespace oxr;
   if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0) return 0;
-  int splits = 0;  // the most any head grouping uses
-  for (int hpw : {1, 2})
-    if (num_kv_heads % hpw == 0) splits = std::max(splits, splits_for(batch, num_kv_heads, hpw));
-  const size_t units = (size_t)batch * num_kv_heads * splits;
+  // Partials of the largest (batch' * KV * splits) over any head grouping and any batch' <= batch:
+  // smaller batches split their contexts further, and a workspace sized for a batch serves every
+  // smaller one.
+  size_t units = 0;
+  for (int32_t bb = 1; bb <= batch; ++bb)
+    for (int hpw : {1, 2})
+      if (num_kv_heads % hpw == 0)
+        units = std::max(units, (size_t)bb * num_kv_heads * splits_for(bb, num_kv_heads, hpw));
   return units * kRows * (kD + 2) * sizeof(float);
 }
 

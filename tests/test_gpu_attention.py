@@ -86,3 +86,26 @@ def test_single_token_and_mha() -> None:
 def test_max_seq_len_bounds_chunks() -> None:
     announce("attention max_seq_len")
     _run([600, 1200], 4, 16, 8, 16, 1024, seed=36, table_width=200, max_seq_len=1300)
+
+
+def test_workspace_sized_for_a_batch_serves_smaller_batches() -> None:
+    """One workspace, sized for the largest batch, serves calls of smaller batches (which split
+    their contexts further) and different contexts in a row; each output equals the output with a
+    fresh workspace of its own, bit for bit."""
+    rng = np.random.default_rng(5)
+    H, KV, S, bs, num_blocks = 16, 8, 4, 16, 4096
+    kc = torch.randn(num_blocks, bs, KV, 128, device="cuda").to(torch.bfloat16)
+    vc = torch.randn(num_blocks, bs, KV, 128, device="cuda").to(torch.bfloat16)
+    max_len = 4096
+    shared = torch.empty(attention.workspace_bytes(16, KV, max_len), dtype=torch.uint8, device="cuda")
+    for batch in (8, 3, 16, 1, 8, 16):
+        seq = rng.integers(S, max_len, size=batch).astype(np.int32)
+        seq[0] = max_len  # the longest context uses every split
+        table = rng.integers(0, num_blocks, size=(batch, max_len // bs)).astype(np.int32)
+        q = torch.randn(batch, S, H, 128, device="cuda").to(torch.bfloat16)
+        seq_t, table_t = torch.from_numpy(seq).cuda(), torch.from_numpy(table).cuda()
+        announce("shared workspace", batch)
+        got = attention.paged_extend(q, kc, vc, seq_t, table_t, max_seq_len=max_len, workspace=shared)
+        fresh = attention.paged_extend(q, kc, vc, seq_t, table_t, max_seq_len=max_len)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), fresh.view(torch.int16)), f"batch {batch}"
