@@ -17,12 +17,30 @@ import torch
 BLOCK_SIZE = 256  # kv_cache.py:19 default
 
 
-class KVCache:
-    """Pages of ``block_size`` tokens; ``allocate``/``release`` may be called from several threads."""
+def _shape_args(first, rest: tuple, what: str) -> tuple[int, int, int, tuple]:
+    """(layers, kv heads, head dim, remaining args) from either call form: the reference's
+    ``(config, ...)`` or explicit ``(num_layers, num_kv_heads, head_dim, ...)``."""
+    if hasattr(first, "num_kv_heads"):
+        return first.num_layers, first.num_kv_heads, first.head_dim, rest
+    if len(rest) < 2:
+        raise TypeError(f"{what}: pass a config, or num_layers, num_kv_heads and head_dim")
+    return int(first), int(rest[0]), int(rest[1]), rest[2:]
 
-    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, num_blocks: int, *,
-                 dtype: torch.dtype = torch.bfloat16, device: torch.device | str = "cuda",
-                 block_size: int = BLOCK_SIZE, fill: float | None = None):
+
+class KVCache:
+    """Pages of ``block_size`` tokens; ``allocate``/``release`` may be called from several threads.
+
+    ``KVCache(config, num_blocks, *, dtype, device)`` is the reference's call (kv_cache.py:26-32);
+    ``KVCache(num_layers, num_kv_heads, head_dim, num_blocks, ...)`` names the shape directly.
+    ``block_size`` (default 256, the reference's) and ``fill`` (initial contents; default
+    uninitialised) are keywords of both."""
+
+    def __init__(self, config_or_layers, *args, dtype: torch.dtype = torch.bfloat16,
+                 device: torch.device | str = "cuda", block_size: int = BLOCK_SIZE, fill: float | None = None):
+        num_layers, num_kv_heads, head_dim, rest = _shape_args(config_or_layers, args, "KVCache")
+        if len(rest) != 1:
+            raise TypeError("KVCache: num_blocks is required (and the only other positional argument)")
+        num_blocks = int(rest[0])
         shape = (num_layers, num_blocks, block_size, num_kv_heads, head_dim)
         make = torch.empty if fill is None else (lambda s, **kw: torch.full(s, fill, **kw))
         self.k = make(shape, dtype=dtype, device=device)
@@ -33,9 +51,14 @@ class KVCache:
         self._lock = threading.Lock()
 
     @staticmethod
-    def bytes_per_block(num_layers: int, num_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.bfloat16,
+    def bytes_per_block(config_or_layers, *args, dtype: torch.dtype | None = None,
                         block_size: int = BLOCK_SIZE) -> int:
-        element = torch.empty((), dtype=dtype).element_size()
+        """K + V bytes of one page over all layers: ``bytes_per_block(config, dtype)`` as in the
+        reference (kv_cache.py:34-37), or ``bytes_per_block(num_layers, num_kv_heads, head_dim[, dtype])``."""
+        num_layers, num_kv_heads, head_dim, rest = _shape_args(config_or_layers, args, "bytes_per_block")
+        if rest:
+            dtype = rest[0]
+        element = torch.empty((), dtype=dtype or torch.bfloat16).element_size()
         return 2 * num_layers * block_size * num_kv_heads * head_dim * element
 
     @property

@@ -107,6 +107,59 @@ class LanguageWeights:
         """Every GEMM matrix row-major again; other tensors shared."""
         return self._map_matrices(lambda w: w.unpack() if isinstance(w, gemm.PackedWeight) else w)
 
+    @classmethod
+    def from_state_dict(cls, config: LanguageConfig, state: dict[str, torch.Tensor], max_positions: int, *,
+                        device=None, dtype: torch.dtype = torch.bfloat16) -> "LanguageWeights":
+        """The reference ``LanguageModel``'s parameters by name (language.py:155-158, 221-231):
+        ``embed_tokens``, ``layers.{i}.{input_layernorm, q_proj, k_proj, v_proj, o_proj, q_norm,
+        k_norm, post_attention_layernorm, gate_proj, up_proj, down_proj}``, ``norm``, ``lm_head``
+        (each ``.weight``); after the reference's ``fuse_projections`` (language.py:234-245)
+        ``qkv_proj`` / ``gate_up_proj`` instead of the split ones.  q/k/v and gate/up are
+        concatenated in that order, as ``fuse_projections`` does.  Every name must be used exactly
+        once and every shape must match, else ``KeyError`` / ``ValueError`` (the reference loader's
+        rules, weights.py:17-44).  The RoPE tables are computed (the reference's are non-persistent
+        buffers, language.py:160-165)."""
+        c = config
+        used: set[str] = set()
+
+        def take(name: str, shape: tuple[int, ...]) -> torch.Tensor:
+            if name not in state:
+                raise KeyError(f"missing parameter {name}")
+            t = state[name]
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
+            used.add(name)
+            return t.to(device=device if device is not None else t.device, dtype=dtype).contiguous()
+
+        def fused(prefix: str, fused_name: str, parts: list[tuple[str, int]], cols: int) -> torch.Tensor:
+            rows = sum(n for _, n in parts)
+            if f"{prefix}{fused_name}.weight" in state:
+                return take(f"{prefix}{fused_name}.weight", (rows, cols))
+            return torch.cat([take(f"{prefix}{name}.weight", (n, cols)) for name, n in parts])
+
+        h, d = c.hidden_size, c.head_dim
+        layers = []
+        for i in range(c.num_layers):
+            p = f"layers.{i}."
+            layers.append(LayerWeights(
+                take(p + "input_layernorm.weight", (h,)),
+                fused(p, "qkv_proj", [("q_proj", c.num_heads * d), ("k_proj", c.num_kv_heads * d),
+                                      ("v_proj", c.num_kv_heads * d)], h),
+                take(p + "q_norm.weight", (d,)), take(p + "k_norm.weight", (d,)),
+                take(p + "o_proj.weight", (h, c.num_heads * d)),
+                take(p + "post_attention_layernorm.weight", (h,)),
+                fused(p, "gate_up_proj", [("gate_proj", c.intermediate_size), ("up_proj", c.intermediate_size)], h),
+                take(p + "down_proj.weight", (h, c.intermediate_size)),
+            ))
+        embed = take("embed_tokens.weight", (c.vocab_size, h))
+        final_norm = take("norm.weight", (h,))
+        head = take("lm_head.weight", (c.vocab_size, h))
+        unused = sorted(set(state) - used - {"rope_cos", "rope_sin"})
+        if unused:
+            raise KeyError(f"parameters with no place in the model: {unused[:8]}{' ...' if len(unused) > 8 else ''}")
+        cos, sin = rope_tables(c, max_positions)
+        return cls(embed, layers, final_norm, head, cos.to(embed.device), sin.to(embed.device))
+
 
 def rope_tables(config: LanguageConfig, max_positions: int) -> tuple[torch.Tensor, torch.Tensor]:
     """language.py:160-170: fp32 angles ``position * theta^(-2i/D)``, cos/sin, stored as bf16."""
