@@ -486,10 +486,15 @@ __global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(cons
 }
 
 // Context splits per (sequence, group of `hpw` kv heads): about one 8-wave
-// workgroup per CU over the whole batch.
-int splits_for(int32_t batch, int32_t num_kv_heads, int hpw) {
+// workgroup per CU over the whole batch, but at least kMinSplitKeys keys of
+// the longest context per split.  (At B = 1, 256 workgroups would leave 64
+// keys each: the launch is then fixed cost, and the merge walks 64 partials.)
+constexpr int kMinSplitKeys = 256;
+int splits_for(int32_t batch, int32_t num_kv_heads, int hpw, int32_t max_seq_len) {
   const int64_t units = (int64_t)batch * (num_kv_heads / hpw);
   int64_t splits = (256 + units - 1) / units;
+  const int64_t by_keys = ((int64_t)max_seq_len + kMinSplitKeys - 1) / kMinSplitKeys;
+  splits = splits < by_keys ? splits : by_keys;
   return (int)(splits < 1 ? 1 : (splits > 64 ? 64 : splits));
 }
 
@@ -526,7 +531,7 @@ extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv
   for (int32_t bb = 1; bb <= batch; ++bb)
     for (int hpw : {1, 2})
       if (num_kv_heads % hpw == 0)
-        units = std::max(units, (size_t)bb * num_kv_heads * splits_for(bb, num_kv_heads, hpw));
+        units = std::max(units, (size_t)bb * num_kv_heads * splits_for(bb, num_kv_heads, hpw, max_seq_len));
   return units * kRows * (kD + 2) * sizeof(float);
 }
 
@@ -554,7 +559,7 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
   OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535 || num_blocks > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
   const int hpw = pick_hpw(tokens_per_seq, num_heads, num_kv_heads);
-  const int splits = splits_for(batch, num_kv_heads, hpw);
+  const int splits = splits_for(batch, num_kv_heads, hpw, max_seq_len);
   {
     // One split's page-table range must fit the kernel's LDS copy.
     const int64_t span_max = ((max_seq_len + splits - 1) / splits + 31) / 32 * 32;
