@@ -15,11 +15,12 @@
 //   one kv head, 128 / G consecutive positions each; wave w owns rows
 //   32w .. 32w + 31 (one per MFMA column; row rho is head slot rho / (128 / G),
 //   position q0 + rho % (128 / G)).
-// * Key tiles of 64 rows are loaded cooperatively (four 16-byte pieces of K
-//   and of V per thread), written to LDS row-major with 16-byte stores,
-//   double-buffered: tile t + 1 is in registers while tile t is multiplied.
-//   Row pitches 68 dwords (K) and 80 dwords (V) make the fragment reads below
-//   free of bank conflicts (measured on gfx950 for exactly these patterns).
+// * Key tiles of 64 rows go from memory straight into LDS (gfx950's 16-byte
+//   global_load_lds: no staging registers, no LDS store instructions),
+//   double-buffered: tile t + 1 is in flight while tile t is multiplied.  Rows
+//   are unpadded with rotated 16-byte chunks, which gives the fragment reads
+//   the banks of 68-dword (K) and 80-dword (V) row pitches, measured free of
+//   bank conflicts on gfx950 for exactly these patterns.
 // * Per wave and tile: S^T = K Q^T (16 MFMAs: 2 key blocks x 8 dim steps;
 //   lane (n, h) holds keys 32kb + 8(v/4) + 4h + v%4 for query n), an
 //   exp2-domain online softmax, then O^T += V^T P^T (16 MFMAs: 4 dim blocks x
@@ -39,9 +40,7 @@ constexpr int kVD = 128;               // head dim
 constexpr int kVWaves = 4;             // waves per workgroup
 constexpr int kVRows = 32 * kVWaves;   // query rows per workgroup (all q heads of the kv head)
 constexpr int kKeyTile = 64;           // keys per LDS stage
-constexpr int kKPitch = kVD + 8;       // bf16 per K row in LDS (68 dwords)
-constexpr int kVPitch = kVD + 32;      // bf16 per V row in LDS (80 dwords)
-constexpr int kPieces = kKeyTile * kVD / 8 / (64 * kVWaves);  // 16-byte pieces of K (and of V) per thread
+constexpr int kLoadsPerWave = kKeyTile * kVD * 2 / 1024 / kVWaves;  // 1 KiB direct-to-LDS loads per wave and tensor
 
 __device__ __forceinline__ f32x16 mfma_32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
@@ -63,8 +62,10 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ cu_seqlens, int H, int KV, int num_qtiles, float scale_log2,
     bf16_t* __restrict__ out) {
-  __shared__ bf16_t s_k[2][kKeyTile][kKPitch];
-  __shared__ bf16_t s_v[2][kKeyTile][kVPitch];
+  // Two buffers per tensor, as separate arrays: the loop below is unrolled by two, so each buffer is
+  // named statically and the compiler can tell a prefetch into one from reads of the other.
+  __shared__ bf16_t s_k0[kKeyTile * kVD], s_k1[kKeyTile * kVD];
+  __shared__ bf16_t s_v0[kKeyTile * kVD], s_v1[kKeyTile * kVD];
 
   // Workgroup b runs on XCD b % 8 (round-robin dispatch).  XCD x takes the x-th eighth of the
   // work items, in order, so the query tiles resident on one XCD at a time belong to one or two
@@ -109,25 +110,24 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   const int key_end = kCausal ? min(len, q0 + rph) : len;  // keys this workgroup needs
   const int tiles = (key_end + kKeyTile - 1) / kKeyTile;
 
-  // Cooperative staging: 16-byte piece p = t + 256u (u < 4) of the tile is dims
-  // [8 (p % 16), +8) of key p / 16, from K and from V (a wave covers 4 whole
-  // rows); keys past the sequence re-read its last key (their scores are masked).
-  const int st_key = tid >> 4, st_d = (tid & 15) * 8;
-  u32x4 kr[kPieces], vr[kPieces];
-  auto fetch = [&](int t) {
+  // Key tiles go straight from memory to LDS (global_load_lds, 16 bytes per lane: lane i of an
+  // instruction writes bytes [16i, 16i + 16) of a 1 KiB block, i.e. 4 rows of 256 bytes).  Rows
+  // are stored without padding, their 16-byte chunks rotated instead: K row r holds chunk c at
+  // position (c + r) mod 16, V row r at (c + 4r) mod 16.  That gives every fragment read below the
+  // banks of a 68-dword (K) or 80-dword (V) row pitch, the ones measured free of conflicts for
+  // these patterns.  Keys past the sequence re-read its last key (their scores are masked).
+  auto dma = [&](int t, bf16_t* kdst, bf16_t* vdst) {
 #pragma unroll
-    for (int u = 0; u < kPieces; ++u) {
-      const int key = min(t * kKeyTile + st_key + 16 * u, len - 1);
-      const int64_t row = ((int64_t)(start + key) * KV + kvh) * kVD + st_d;
-      kr[u] = ld128(k + row);
-      vr[u] = ld128(v + row);
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < kPieces; ++u) {
-      *reinterpret_cast<u32x4*>(&s_k[buf][st_key + 16 * u][st_d]) = kr[u];
-      *reinterpret_cast<u32x4*>(&s_v[buf][st_key + 16 * u][st_d]) = vr[u];
+    for (int u = 0; u < kLoadsPerWave; ++u) {
+      const int j = kLoadsPerWave * wave + u;  // 1 KiB block: rows 4j .. 4j + 3
+      const int row = 4 * j + (lane >> 4), pos = lane & 15;
+      const int key = min(t * kKeyTile + row, len - 1);
+      const int64_t base = ((int64_t)(start + key) * KV + kvh) * kVD;
+      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(k + base + 8 * ((pos - row) & 15)),
+                                       (void __attribute__((address_space(3)))*)(kdst + 512 * j), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(v + base + 8 * ((pos - 4 * row) & 15)),
+          (void __attribute__((address_space(3)))*)(vdst + 512 * j), 16, 0, 0);
     }
   };
 
@@ -139,16 +139,18 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
 
   // Transposing-read address of lane (n, h) for V^T fragment (dim block dt, key step ks, half p):
-  // lane j of its 16-lane group addresses key 16ks + 8p + 4h + j / 4, dims 32dt + 16 (n / 16) + 4 (j % 4).
+  // lane j of its 16-lane group addresses key 16ks + 8p + 4h + j / 4, dims 32dt + 16 (n / 16) + 4 (j % 4),
+  // i.e. chunk 4dt + 2 (n / 16) + (j % 4) / 2 of its row, half (j % 2); the row's rotation is 4 tr_key
+  // (mod 16) for every (ks, p).
   const int tr_key = 4 * h + ((lane & 15) >> 2);
-  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int tr_off[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+    tr_off[dt] = 8 * ((4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1) + 4 * tr_key) & 15) + 4 * (lane & 1);
 
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int t = 0; t < tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < tiles) fetch(t + 1);  // in flight during this tile's products
+  // One key tile: products from K and V in LDS (kb, vb), prefetch of the next tile into (kn, vn).
+  auto tile = [&](int t, const bf16_t* kb_, const bf16_t* vb_, bf16_t* kn, bf16_t* vn) {
+    if (t + 1 < tiles) dma(t + 1, kn, vn);  // in flight during this tile's products
     const int kt0 = t * kKeyTile;
     if (kt0 <= wave_last) {  // wave-uniform: otherwise every key of the tile is masked for this wave
       // Raw scores: sv[kb][v] is key kt0 + 32kb + 8(v/4) + 4h + v%4 for query n.
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(&s_k[buf][32 * kb + n][16 * i + 8 * h]);
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(kb_ + (32 * kb + n) * kVD + 8 * ((2 * i + h + n) & 15));
           sv[kb] = mfma_32x32x16(kf, qf[i], sv[kb]);
         }
       // wave-uniform: a tile crossing the diagonal of one of the wave's rows, or the sequence end
@@ -218,17 +220,27 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
       l_run += ps[0];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16_t* vp = &s_v[buf][16 * ks + tr_key][tr_dim];
+        const bf16_t* vp = vb_ + (16 * ks + tr_key) * kVD;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const u32x2 lo = lds_read_tr16(vp + 32 * dt);                // keys 16ks + 4h + (0..3)
-          const u32x2 hi = lds_read_tr16(vp + 8 * kVPitch + 32 * dt);  // keys 16ks + 8 + 4h + (0..3)
+          const u32x2 lo = lds_read_tr16(vp + tr_off[dt]);            // keys 16ks + 4h + (0..3)
+          const u32x2 hi = lds_read_tr16(vp + 8 * kVD + tr_off[dt]);  // keys 16ks + 8 + 4h + (0..3)
           o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[ks], o[dt]);
         }
       }
     }
-    if (t + 1 < tiles) stash(buf ^ 1);  // the other buffer was last read before the previous barrier
+    // The next tile's loads (into the buffers last read before the previous barrier) have landed in
+    // LDS once this wave's vector memory count drains; the barrier publishes every wave's.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+
+  dma(0, s_k0, s_v0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int t = 0; t < tiles; t += 2) {
+    tile(t, s_k0, s_v0, s_k1, s_v1);
+    if (t + 1 < tiles) tile(t + 1, s_k1, s_v1, s_k0, s_v0);
   }
 
   // Normalise and store: lane (n, h) holds O^T[32dt + 8(e/4) + 4h + e%4][query n].
