@@ -26,7 +26,10 @@
 //   exp2-domain online softmax, then O^T += V^T P^T (16 MFMAs: 4 dim blocks x
 //   4 key steps; P^T is used as computed: k slot 8h + 4p + j of key step ks
 //   stands for key 16ks + 8p + 4h + j).  The V^T fragments come from gfx950's
-//   transposing LDS read (ds_read_b64_tr_b16) of the row-major V tile.
+//   transposing LDS read (ds_read_b64_tr_b16) of the row-major V tile.  The
+//   QK^T products of tile t + 1 are issued among tile t's exponentials (K is
+//   staged one tile ahead of V), so the matrix cores and the vector unit of a
+//   wave overlap.
 // * Causal: key tiles above a wave's last row are skipped, tiles that cross a
 //   row's diagonal are masked per element; keys past the sequence are masked.
 #include "common.h"
@@ -116,18 +119,16 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   // position (c + r) mod 16, V row r at (c + 4r) mod 16.  That gives every fragment read below the
   // banks of a 68-dword (K) or 80-dword (V) row pitch, the ones measured free of conflicts for
   // these patterns.  Keys past the sequence re-read its last key (their scores are masked).
-  auto dma = [&](int t, bf16_t* kdst, bf16_t* vdst) {
+  auto dma = [&](const bf16_t* src, int t, bf16_t* dst, int rot) {
 #pragma unroll
     for (int u = 0; u < kLoadsPerWave; ++u) {
       const int j = kLoadsPerWave * wave + u;  // 1 KiB block: rows 4j .. 4j + 3
       const int row = 4 * j + (lane >> 4), pos = lane & 15;
       const int key = min(t * kKeyTile + row, len - 1);
       const int64_t base = ((int64_t)(start + key) * KV + kvh) * kVD;
-      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(k + base + 8 * ((pos - row) & 15)),
-                                       (void __attribute__((address_space(3)))*)(kdst + 512 * j), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(v + base + 8 * ((pos - 4 * row) & 15)),
-          (void __attribute__((address_space(3)))*)(vdst + 512 * j), 16, 0, 0);
+          (const void __attribute__((address_space(1)))*)(src + base + 8 * ((pos - rot * row) & 15)),
+          (void __attribute__((address_space(3)))*)(dst + 512 * j), 16, 0, 0);
     }
   };
 
@@ -148,25 +149,33 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   for (int dt = 0; dt < 4; ++dt)
     tr_off[dt] = 8 * ((4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1) + 4 * tr_key) & 15) + 4 * (lane & 1);
 
-  // One key tile: products from K and V in LDS (kb, vb), prefetch of the next tile into (kn, vn).
-  auto tile = [&](int t, const bf16_t* kb_, const bf16_t* vb_, bf16_t* kn, bf16_t* vn) {
-    if (t + 1 < tiles) dma(t + 1, kn, vn);  // in flight during this tile's products
+  // Raw scores of one tile: sv[kb][v] is key 32kb + 8(v/4) + 4h + v%4 of the tile for query n.  The
+  // two key blocks' chains alternate, so consecutive products are independent.
+  auto qk = [&](const bf16_t* kb_, f32x16 (&sv)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sv[kb][e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(kb_ + (32 * kb + n) * kVD + 8 * ((2 * i + h + n) & 15));
+        sv[kb] = mfma_32x32x16(kf, qf[i], sv[kb]);
+      }
+  };
+
+  // Tile t, software-pipelined by one tile: its scores `cur` were computed during tile t - 1; the
+  // products for tile t + 1's scores `nxt` (K in kq) are issued among this tile's exponentials, so
+  // the matrix cores work while the softmax runs on the vector unit.  K runs one tile ahead of V in
+  // the double buffers: tile t prefetches K(t + 2) into kd and V(t + 1) into vd, the buffers read
+  // during tile t - 1.  Past the last tile `nxt` is computed from a stale buffer and never used.
+  auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2], const bf16_t* kq, const bf16_t* vp_, bf16_t* kd,
+                  bf16_t* vd) {
+    if (t + 2 < tiles) dma(k, t + 2, kd, 1);
+    if (t + 1 < tiles) dma(v, t + 1, vd, 4);
     const int kt0 = t * kKeyTile;
-    if (kt0 <= wave_last) {  // wave-uniform: otherwise every key of the tile is masked for this wave
-      // Raw scores: sv[kb][v] is key kt0 + 32kb + 8(v/4) + 4h + v%4 for query n.
-      // The two key blocks' chains alternate, so consecutive products are independent.
-      f32x16 sv[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sv[kb][e] = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(kb_ + (32 * kb + n) * kVD + 8 * ((2 * i + h + n) & 15));
-          sv[kb] = mfma_32x32x16(kf, qf[i], sv[kb]);
-        }
+    if (kt0 <= wave_last) {  // wave-uniform: otherwise every key of this and later tiles is masked
       // wave-uniform: a tile crossing the diagonal of one of the wave's rows, or the sequence end
       const bool edge = (kCausal && kt0 + kKeyTile - 1 > wave_first) || kt0 + kKeyTile > len;
       if (edge) {
@@ -175,17 +184,17 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int key = kt0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (key >= len || (kCausal && key > qpos)) sv[kb][e] = -INFINITY;
+            if (key >= len || (kCausal && key > qpos)) cur[kb][e] = -INFINITY;
           }
       }
       // Row maximum as a tree (max is exact in any order).
       float mt[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mt[e] = fmaxf(sv[0][e], sv[1][e]);
+      for (int e = 0; e < 16; ++e) mt[e] = fmaxf(cur[0][e], cur[1][e]);
 #pragma unroll
-      for (int w = 8; w >= 1; w >>= 1)
+      for (int w2 = 8; w2 >= 1; w2 >>= 1)
 #pragma unroll
-        for (int e = 0; e < w; ++e) mt[e] = fmaxf(mt[e], mt[e + w]);
+        for (int e = 0; e < w2; ++e) mt[e] = fmaxf(mt[e], mt[e + w2]);
       const float mx = fmaxf(mt[0], shfl_xor_f(mt[0], 32));
       const bool moved = mx > m_run;
       if (__builtin_amdgcn_ballot_w64(moved)) {
@@ -198,6 +207,7 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
         m_run = m_new;
         mc_run = mc_new;
       }
+      qk(kq, nxt);
       // P^T for key step ks: accumulators 8 (ks % 2) .. +7 of key block ks / 2, in k-slot order.
       // The tile's probabilities are summed as a tree, then added to the running sum.
       u32x4 pb[4];
@@ -207,40 +217,44 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
         float pv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[ks >> 1][8 * (ks & 1) + e], scale_log2, -mc_run));
+          pv[e] = __builtin_amdgcn_exp2f(fmaf(cur[ks >> 1][8 * (ks & 1) + e], scale_log2, -mc_run));
 #pragma unroll
         for (int e = 0; e < 4; ++e) ps[4 * ks + e] = pv[e] + pv[e + 4];
         pb[ks] = u32x4{pack_bf_hw(pv[0], pv[1]), pack_bf_hw(pv[2], pv[3]), pack_bf_hw(pv[4], pv[5]),
                        pack_bf_hw(pv[6], pv[7])};
       }
 #pragma unroll
-      for (int w = 8; w >= 1; w >>= 1)
+      for (int w2 = 8; w2 >= 1; w2 >>= 1)
 #pragma unroll
-        for (int e = 0; e < w; ++e) ps[e] += ps[e + w];
+        for (int e = 0; e < w2; ++e) ps[e] += ps[e + w2];
       l_run += ps[0];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16_t* vp = vb_ + (16 * ks + tr_key) * kVD;
+        const bf16_t* vrow = vp_ + (16 * ks + tr_key) * kVD;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const u32x2 lo = lds_read_tr16(vp + tr_off[dt]);            // keys 16ks + 4h + (0..3)
-          const u32x2 hi = lds_read_tr16(vp + 8 * kVD + tr_off[dt]);  // keys 16ks + 8 + 4h + (0..3)
+          const u32x2 lo = lds_read_tr16(vrow + tr_off[dt]);            // keys 16ks + 4h + (0..3)
+          const u32x2 hi = lds_read_tr16(vrow + 8 * kVD + tr_off[dt]);  // keys 16ks + 8 + 4h + (0..3)
           o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[ks], o[dt]);
         }
       }
     }
-    // The next tile's loads (into the buffers last read before the previous barrier) have landed in
-    // LDS once this wave's vector memory count drains; the barrier publishes every wave's.
+    // This wave's prefetches have landed in LDS once its vector memory count drains; the barrier
+    // publishes every wave's, and ends every read of the buffers the next tile prefetches into.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
 
-  dma(0, s_k0, s_v0);
+  f32x16 sa[2], sb[2];
+  dma(k, 0, s_k0, 1);
+  if (tiles > 1) dma(k, 1, s_k1, 1);
+  dma(v, 0, s_v0, 4);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  qk(s_k0, sa);
   for (int t = 0; t < tiles; t += 2) {
-    tile(t, s_k0, s_v0, s_k1, s_v1);
-    if (t + 1 < tiles) tile(t + 1, s_k1, s_v1, s_k0, s_v0);
+    step(t, sa, sb, s_k1, s_v0, s_k0, s_v1);
+    if (t + 1 < tiles) step(t + 1, sb, sa, s_k0, s_v1, s_k1, s_v0);
   }
 
   // Normalise and store: lane (n, h) holds O^T[32dt + 8(e/4) + 4h + e%4][query n].
