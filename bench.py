@@ -39,6 +39,9 @@ kv_cache = importlib.import_module(f"{PKG}.kv_cache")
 decode_graph = importlib.import_module(f"{PKG}.decode_graph")
 attention = importlib.import_module(f"{PKG}.attention")
 gemm = importlib.import_module(f"{PKG}.gemm")
+kernels = importlib.import_module(f"{PKG}.kernels")
+lm_head = importlib.import_module(f"{PKG}.lm_head")
+speculative = importlib.import_module(f"{PKG}.speculative")
 workloads = importlib.import_module(f"{PKG}.workloads")
 
 METRIC = "accepted tokens/sec + verify-step latency (us) at B=8,k=3; % HBM roofline"
@@ -198,6 +201,89 @@ def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, see
             "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
 
 
+def _time_us(fn, iters: int = 20, per_graph: int = 10) -> float:
+    """GPU time of one ``fn`` call: ``per_graph`` calls captured in a HIP graph, replayed ``iters``
+    times between HIP events on the replay stream (so host launch overhead is not measured)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(per_graph):
+            fn()
+    torch.cuda.synchronize()
+    graph.replay()
+    stream = torch.cuda.current_stream()  # where replay() launches the graph
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / (iters * per_graph)
+
+
+def time_configs(config, lm_weight, seed: int = 0) -> dict:
+    """The benchmark's per-kernel configurations (2 and 4) on the GPU path, inputs
+    resident on the device.  Config 3 is the ``roofline`` launch and config 5 the step itself."""
+    rng = np.random.default_rng(seed)
+    dev = "cuda"
+    res = {}
+
+    # Config 1: drafting (max_n 3, k 3) over 4 histories of 512 tokens, then acceptance.
+    hist = torch.from_numpy(workloads.drafting_histories(seed, 4, 512)).to(dev)
+    hlen = torch.full((4,), 512, dtype=torch.int32, device=dev)
+    draft, dlen = speculative.propose_batch(hist, hlen, 3, max_n=3)
+    predicted = torch.from_numpy(rng.integers(0, config.vocab_size, size=(4, 4))).to(dev)
+    us_d = _time_us(lambda: speculative.propose_batch(hist, hlen, 3, max_n=3, draft=draft, draft_len=dlen))
+    us_a = _time_us(lambda: speculative.accept_batch(draft, dlen, predicted))
+    res["config1_draft_accept"] = {"draft_us": us_d, "accept_us": us_a, "batch": 4, "history": 512, "max_n": 3, "k": 3}
+
+    # Config 2: fused q/k RMSNorm + RoPE + paged KV write, 32 sequences x 4 tokens, 65,536-block pool.
+    t, h, kv, d = 128, config.num_heads, config.num_kv_heads, config.head_dim
+    pb = workloads.paged_batch(rng, 32, 4, (256, 4096), block_size=16, num_blocks=65_536)
+    kc = torch.zeros(65_536, 16, kv, d, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qkv = torch.randn(t, (h + 2 * kv) * d, device=dev).to(torch.bfloat16)
+    qw = (0.5 + torch.rand(d, device=dev)).to(torch.bfloat16)
+    kw = (0.5 + torch.rand(d, device=dev)).to(torch.bfloat16)
+    cos_t, sin_t = language.rope_tables(config, 4096)
+    pos = torch.from_numpy(pb.positions).to(dev)
+    cos, sin = cos_t.to(dev)[pos].contiguous(), sin_t.to(dev)[pos].contiguous()
+    slots = torch.from_numpy(pb.slots).to(dev)
+    q_out = torch.empty(t, h, d, dtype=torch.bfloat16, device=dev)
+    us = _time_us(lambda: kernels.qk_norm_rope_store(qkv, qw, kw, cos, sin, 1e-6, kc, vc, slots, h, kv, d,
+                                                     need_kv=False, q_out=q_out))
+    nbytes = 2_131_456
+    res["config2_qk_norm_rope_store"] = {"us": us, "bytes": nbytes, "achieved": nbytes / (us * 1e-6) / 1e9,
+                                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                         "frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    del kc, vc
+
+    # Config 4: LM head + vocab argmax over 64 sequences x 4 positions, then acceptance (k = 3).
+    rows = 256
+    hidden = torch.randn(rows, config.hidden_size, device=dev).to(torch.bfloat16)
+    pred = torch.empty(rows, dtype=torch.int64, device=dev)
+    ws = torch.empty(max(lm_head.workspace_bytes(rows, config.vocab_size), 1), dtype=torch.uint8, device=dev)
+    us_h = _time_us(lambda: lm_head.lm_head_argmax(hidden, lm_weight, predicted=pred, workspace=ws))
+    drafts4 = torch.from_numpy(rng.integers(0, config.vocab_size, size=(64, 3)).astype(np.int32)).to(dev)
+    dlen4 = torch.full((64,), 3, dtype=torch.int32, device=dev)
+    us_a4 = _time_us(lambda: speculative.accept_batch(drafts4, dlen4, pred.view(64, 4)))
+    wbytes = config.vocab_size * config.hidden_size * 2 + rows * config.hidden_size * 2
+    flops = 2.0 * rows * config.hidden_size * config.vocab_size
+    res["config4_lm_head_accept"] = {
+        "rows": rows, "lm_head_us": us_h, "accept_us": us_a4, "bytes": wbytes,
+        "hbm_achieved": wbytes / (us_h * 1e-6) / 1e9, "hbm_frac": wbytes / (us_h * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "mfma_achieved_tflops": flops / (us_h * 1e-6) / 1e12,
+        "mfma_frac": flops / (us_h * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+    return res
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per attention launch from the committed rocprofv3 --pmc summary (FETCH_SIZE +
     WRITE_SIZE of both kernels, each scaled by the counter's reading for a copy of known size)."""
@@ -283,6 +369,7 @@ def main() -> int:
     p.add_argument("--pmc-driver", action="store_true", help="only attention launches + a calibration copy")
     p.add_argument("--cpu-warmup", type=int, default=1)
     p.add_argument("--prefill-driver", action="store_true", help="only the prefill attention measurement")
+    p.add_argument("--configs-driver", action="store_true", help="only the per-kernel configurations 1, 2 and 4")
     args = p.parse_args()
 
     if args.gpus != 1:
@@ -297,6 +384,11 @@ def main() -> int:
 
     if args.prefill_driver:
         print(json.dumps(time_prefill(language.QWEN_SYNTHETIC)), flush=True)
+        return 0
+    if args.configs_driver:
+        c = language.QWEN_SYNTHETIC
+        w = gemm.pack_weight((torch.randn(c.vocab_size, c.hidden_size, device=device) * 0.02).to(torch.bfloat16))
+        print(json.dumps(time_configs(c, w, args.seed)), flush=True)
         return 0
     log("building workload")
     config, model, cache, table, histories, seq_lens, width = build_workload(args, device)
@@ -340,6 +432,8 @@ def main() -> int:
     log(f"decode step (B={decode['batch']}, one token each) {decode['step_us']:.1f} us")
     prefill = time_prefill(config)
     log(f"prefill attention {prefill['us']:.1f} us, {prefill['achieved']:.0f} TFLOP/s")
+    configs = time_configs(config, model.weights.lm_head, args.seed)
+    log("configs: " + json.dumps(configs))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -381,6 +475,7 @@ def main() -> int:
                         "achieved": decode["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": decode["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill_attention": prefill,
+        "configs": configs,
         "cpu_baseline": cpu,
         "wall_s_timed": wall,
     }

@@ -254,8 +254,11 @@ int oxr_gemm_bf16_partial(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_b
  * the largest bf16 logit of row i (NaN counts as largest, -0 == +0).
  * hidden bf16 [m, hidden_size]; weight bf16 [vocab, hidden_size]; predicted
  * int64 [m].  logits (optional, bf16 [m, vocab]) receives the bf16 logits.
- * m <= 64; hidden_size a multiple of 128.  workspace: at least
- * oxr_lm_head_workspace_bytes(m, vocab) bytes (per-tile maxima).
+ * m <= 64 (up to 256 with oxr_lm_head_argmax_packed and hidden_size 512,
+ * 1024 or 2048: one launch then reads the weight once for all rows);
+ * hidden_size a multiple of 128.  workspace: at least
+ * oxr_lm_head_workspace_bytes(m, vocab) bytes (per-tile maxima; for more
+ * than 32 rows also room for the rows repacked).
  */
 size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab);
 int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,

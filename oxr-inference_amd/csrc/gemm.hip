@@ -455,6 +455,238 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_lds_kernel(const bf16_t
   }
 }
 
+// ---------------------------------------------------------------------------
+// LM head for 33..256 token rows (packed weight): with M = 256 the head does
+// 159 GFLOP on 622 MB, close to the MFMA/HBM ridge, so the products use the
+// 32x32x16 MFMA (twice the work per issue of the 16x16x32 form on gfx950) and
+// the weight is still read exactly once.  One persistent workgroup per CU
+// owns a balanced contiguous range of 32-row vocab tiles, taken 8 at a time
+// (a group): wave w multiplies vocab tile w of the group by all token rows
+// (128 accumulators and a 2-chunk weight ring per wave).
+// * Each wave streams its own weight rows straight into registers through a
+//   kWideDepth-chunk ring (64 k per chunk; a lane's 16-byte fragment of the
+//   packed layout -- four contiguous 256-byte runs per instruction).
+// * The token rows (packed by the entry point into the workspace) are shared
+//   by all 8 waves: chunk by chunk, loaded straight into LDS (four buffers,
+//   two chunks ahead of use -- at least as far ahead as the weight ring, so
+//   that waiting for a chunk (the vector memory counter is in order) never
+//   waits for a weight chunk that is not due yet -- one
+//   barrier per chunk) in the packed order, so each 16-lane fragment read is
+//   one contiguous 256-byte run.
+// * Epilogue per group: bf16-rounded logits -> per-token best keys, merged
+//   into the wave's slot in LDS; at the end one key per token per workgroup,
+//   reduced across workgroups by argmax_reduce_kernel.
+// ---------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWideWaves = 8;      // waves per workgroup (two per SIMD) = vocab tiles per group
+constexpr int kWideTokTiles = 8;   // 32-token tiles (M <= 256)
+constexpr int kWideChunk = 64;     // k per stage
+constexpr int kWideDepth = 2;      // weight chunks in flight per wave (two waves per SIMD: 256 registers)
+constexpr int kXBlocksPerWave = 32 / kWideWaves;  // 1 KiB blocks of a token-row chunk staged per wave
+constexpr int kUnroll = 8;         // stages per unrolled step: ring slot and LDS buffer fixed per position
+constexpr int kWideMaxGrid = 1024; // bound on the workgroups (sizes the workspace)
+constexpr int kWideMaxRows = 32 * kWideTokTiles;
+
+// s_waitcnt immediate (gfx9 encoding) waiting until at most `n` vector memory operations are outstanding,
+// with the other counters unconstrained: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+__device__ __forceinline__ f32x16 mfma_32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+// TT: 32-token tiles computed (2, 4 or 8; rows past M are padding whose results nobody reads).
+template <int K, int TT>
+__global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf16_t* __restrict__ xp, int M,
+                                                                      const bf16_t* __restrict__ w, int64_t N,
+                                                                      bf16_t* __restrict__ logits, int64_t ldl,
+                                                                      uint64_t* __restrict__ best_out) {
+  constexpr int kChunks = K / kWideChunk;
+  static_assert(K % 128 == 0, "packed k steps are 128 wide");
+  // X chunk: token row tile t (16 tokens) x block i (32 k) at (2t + i) * 512 elements, lane order inside.
+  // Four buffers (stage s reads s % 4; chunks go in two stages ahead), as separate arrays so the compiler
+  // can tell a load into one from reads of another.
+  __shared__ bf16_t xs0[kWideTokTiles * 2 * 2 * 512], xs1[kWideTokTiles * 2 * 2 * 512];
+  __shared__ bf16_t xs2[kWideTokTiles * 2 * 2 * 512], xs3[kWideTokTiles * 2 * 2 * 512];
+  __shared__ uint64_t wave_best[kWideWaves][kWideMaxRows];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, h = lane >> 5, r = lane & 15;
+  const int x_tiles = (M + 15) / 16;             // packed 16-row token tiles present
+  const int64_t w_last = (N + 15) / 16 - 1;       // last packed 16-row weight tile
+  const int64_t nt32 = (N + 31) / 32;
+  const int64_t lo = (int64_t)blockIdx.x * nt32 / gridDim.x, hi = (int64_t)(blockIdx.x + 1) * nt32 / gridDim.x;
+  const int64_t groups = (hi - lo + kWideWaves - 1) / kWideWaves;
+  const int64_t stages = groups * kChunks;
+
+  for (int i = tid; i < kWideWaves * kWideMaxRows; i += 64 * kWideWaves) (&wave_best[0][0])[i] = 0;
+
+  // Weight fragment of stage s (group s / kChunks, chunk s % kChunks), k16 step kk: lane (n, h) holds
+  // W[32 vt + n][64 c + 16 kk + 8h, +8).  Past this workgroup's range (or a vocab tile it does not own in
+  // its last group) a lane re-reads a valid row whose products nobody uses.
+  auto wfrag = [&](int64_t s, int kk) {
+    s = s < stages ? s : stages - 1;
+    const int64_t gi = s / kChunks;
+    const int c = (int)(s - gi * kChunks);
+    int64_t vt = lo + gi * kWideWaves + wave;
+    vt = vt < hi ? vt : hi - 1;
+    int64_t t = 2 * vt + (n >> 4);
+    t = t < w_last ? t : w_last;
+    const int i = 2 * (c & 1) + (kk >> 1), g = 2 * (kk & 1) + h;
+    return ld128(w + t * (K * 16) + (c >> 1) * (16 * kKStep) + i * 512 + (16 * g + r) * 8);
+  };
+  // Token rows of chunk c straight into an LDS buffer (global_load_lds, 16 bytes per lane: lane i of an
+  // instruction writes bytes [16i, 16i + 16) of a 1 KiB block): 32 blocks (block j: token row tile j / 2,
+  // half j % 2 of the chunk's 64 k), kXBlocksPerWave per wave.  Tiles past the last one re-read it.
+  auto xdma = [&](int c, bf16_t* dst) {
+#pragma unroll
+    for (int u = 0; u < kXBlocksPerWave; ++u) {
+      const int j = kXBlocksPerWave * wave + u, t = j >> 1;
+      const int tl = t < x_tiles ? t : x_tiles - 1;
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(xp + (int64_t)tl * (K * 16) + (c >> 1) * (16 * kKStep) +
+                                                          (2 * (c & 1) + (j & 1)) * 512 + lane * 8),
+          (void __attribute__((address_space(3)))*)(dst + j * 512), 16, 0, 0);
+    }
+  };
+
+  u32x4 ring[kWideDepth][4];
+#pragma unroll
+  for (int d = 0; d < kWideDepth; ++d)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) ring[d][kk] = wfrag(d, kk);
+  // Stage s's token rows go in at stage s - 2 (chunk c of stage s is s % kChunks; past the last stage the
+  // loads repeat a valid chunk into a buffer nobody reads), so every stage issues the same loads: its
+  // token-row block loads, then its 4 weight loads.  At the end of stage s, the loads issued after
+  // stage s + 1's token rows are 4 + (kXBlocksPerWave + 4); everything older has landed.
+  auto xchunk = [&](int64_t st) { return (int)((st < stages ? st : stages - 1) % kChunks); };
+  xdma(xchunk(0), xs0);
+  xdma(xchunk(1), xs1);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(kXBlocksPerWave));
+  __syncthreads();
+
+  f32x16 acc[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[tt][e] = 0.f;
+
+  // Stage s = gi * kChunks + c: chunk c of group gi.  kChunks is a multiple of kWideDepth (even), so
+  // stage s uses ring slot s % kWideDepth and LDS buffer s % 2, both fixed per unrolled position.
+  static_assert(kChunks % kUnroll == 0 && kUnroll % kWideDepth == 0 && kUnroll % 4 == 0,
+                "ring slots and buffers must be static");
+  for (int64_t gi = 0; gi < groups; ++gi) {
+    for (int c0 = 0; c0 < kChunks; c0 += kUnroll) {
+#pragma unroll
+      for (int d = 0; d < kUnroll; ++d) {
+        const int c = c0 + d;
+        const int64_t s = gi * kChunks + c;
+        bf16_t* const bufs[4] = {xs0, xs1, xs2, xs3};
+        xdma(xchunk(s + 2), bufs[(d + 2) & 3]);  // read at stage s - 2, before the last barrier
+        __builtin_amdgcn_sched_barrier(0);
+        const bf16_t* xb = bufs[d & 3];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int off = (kk >> 1) * 512 + (16 * (2 * (kk & 1) + h) + r) * 8;
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt) {
+            const u32x4 bf = *reinterpret_cast<const u32x4*>(xb + (2 * (2 * tt + (n >> 4))) * 512 + off);
+            acc[tt] = mfma_32x32x16(ring[d % kWideDepth][kk], bf, acc[tt]);
+          }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) ring[d % kWideDepth][kk] = wfrag(s + kWideDepth, kk);
+        __builtin_amdgcn_sched_barrier(0);
+        // The only LDS data that crosses waves in the loop is what the token-row loads write, and the
+        // count above covers it; a barrier with fences (or __syncthreads) would also wait for every
+        // weight load in flight.  The memory clobber keeps LDS reads on their side of the barrier.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 + (kXBlocksPerWave + 4)));  // a wait the compiler can count on
+        asm volatile("s_barrier" ::: "memory");
+      }
+    }
+    // Group epilogue: vocab tile vt of this wave; lane (n, h) holds logits of vocab rows
+    // 32 vt + 8 (e / 4) + 4h + e % 4 for token 32 tt + n.
+    const int64_t vt = lo + gi * kWideWaves + wave;
+    if (vt < hi) {  // wave-uniform
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const int tok = 32 * tt + n;
+        uint64_t best = 0;
+#pragma unroll
+        for (int m4 = 0; m4 < 4; ++m4) {
+          const int64_t col0 = 32 * vt + 8 * m4 + 4 * h;
+          uint32_t b16[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            b16[j] = f2bf(acc[tt][4 * m4 + j]);
+            if (col0 + j < N) {
+              const uint64_t key = argmax_key(b16[j] << 16, (uint32_t)(col0 + j));
+              best = key > best ? key : best;
+            }
+          }
+          if (logits && tok < M) {
+            bf16_t* dst = logits + (int64_t)tok * ldl + col0;
+            if (col0 + 3 < N) {
+              *reinterpret_cast<u32x2*>(dst) = u32x2{b16[0] | (b16[1] << 16), b16[2] | (b16[3] << 16)};
+            } else {
+              for (int j = 0; j < 4; ++j)
+                if (col0 + j < N) dst[j] = (bf16_t)b16[j];
+            }
+          }
+        }
+        const uint64_t o = shfl_xor_u64(best, 32);
+        best = o > best ? o : best;
+        if (h == 0 && best > wave_best[wave][tok]) wave_best[wave][tok] = best;
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[tt][e] = 0.f;
+  }
+  __syncthreads();
+
+  if (tid < M) {
+    uint64_t b = 0;
+#pragma unroll
+    for (int wv = 0; wv < kWideWaves; ++wv) b = wave_best[wv][tid] > b ? wave_best[wv][tid] : b;
+    best_out[(int64_t)blockIdx.x * M + tid] = b;
+  }
+}
+
+// Workspace of the wide path: per-workgroup keys (at most kWideMaxGrid workgroups), then the packed token
+// rows (hidden size at most 2048).
+size_t wide_x_offset(int64_t m) { return ((size_t)kWideMaxGrid * (size_t)m * sizeof(uint64_t) + 255) / 256 * 256; }
+size_t wide_workspace_bytes(int64_t m) { return wide_x_offset(m) + (size_t)((m + 15) / 16 * 16) * 2048 * sizeof(bf16_t); }
+
+// Row counts and hidden sizes the wide LM head takes (packed weight only).
+bool lm_head_wide_supported(int64_t m, int64_t k, bool packed) {
+  return packed && m > 32 && m <= kWideMaxRows && (k == 512 || k == 1024 || k == 2048);
+}
+
+template <int TT>
+int launch_lm_head_wide_tt(const bf16_t* xp, int M, const bf16_t* w, int64_t K, int64_t N, bf16_t* logits,
+                           uint64_t* best, int grid, hipStream_t s) {
+  const dim3 g((unsigned)grid), b(64 * kWideWaves);
+  switch (K) {
+    case 512: hipLaunchKernelGGL((lm_head_wide_kernel<512, TT>), g, b, 0, s, xp, M, w, N, logits, N, best); break;
+    case 1024: hipLaunchKernelGGL((lm_head_wide_kernel<1024, TT>), g, b, 0, s, xp, M, w, N, logits, N, best); break;
+    case 2048: hipLaunchKernelGGL((lm_head_wide_kernel<2048, TT>), g, b, 0, s, xp, M, w, N, logits, N, best); break;
+    default: return OXR_ERR_UNSUPPORTED;
+  }
+  return OXR_LAUNCH_STATUS();
+}
+
+int launch_lm_head_wide(const bf16_t* xp, int M, const bf16_t* w, int64_t K, int64_t N, bf16_t* logits,
+                        uint64_t* best, int grid, hipStream_t s) {
+  if (M <= 64) return launch_lm_head_wide_tt<2>(xp, M, w, K, N, logits, best, grid, s);
+  if (M <= 128) return launch_lm_head_wide_tt<4>(xp, M, w, K, N, logits, best, grid, s);
+  return launch_lm_head_wide_tt<8>(xp, M, w, K, N, logits, best, grid, s);
+}
+
 // Compute units of the current device (one persistent LM-head workgroup each).
 int device_cus() {
   static int cached[64] = {0};
@@ -642,7 +874,9 @@ int gemm_partial_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16
 int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
                   oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes, bool packed,
                   oxr_stream_t stream) {
-  int st = check_common(hidden, hidden_size, m, weight, hidden_size, vocab);
+  // More than 64 rows only on the wide path (packed weight, up to 256 rows); the common checks see at most 64.
+  OXR_RETURN_IF(m > 64 && !lm_head_wide_supported(m, hidden_size, packed), OXR_ERR_UNSUPPORTED);
+  int st = check_common(hidden, hidden_size, std::min<int64_t>(m, 64), weight, hidden_size, vocab);
   if (st) return st;
   OXR_RETURN_IF(!predicted, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(logits && (uintptr_t)logits % 8 != 0, OXR_ERR_UNSUPPORTED);
@@ -653,7 +887,17 @@ int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int
   hipStream_t s = (hipStream_t)stream;
   uint64_t* best = static_cast<uint64_t*>(workspace);
   int num_best;  // partial maxima per token for the final reduction
-  if (lm_head_lds_supported(m, hidden_size)) {
+  if (lm_head_wide_supported(m, hidden_size, packed)) {
+    // Token rows packed into the workspace (after the per-workgroup keys), then the wide kernel.
+    const int64_t nt32 = (vocab + 31) / 32;
+    num_best = (int)std::min<int64_t>(std::min(device_cus(), kWideMaxGrid), nt32);
+    bf16_t* xp = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + wide_x_offset(m));
+    const int64_t chunks = (int64_t)oxr_packed_weight_elems(m, hidden_size) / 8;
+    hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)std::min<int64_t>((chunks + 255) / 256, 4096)), dim3(256),
+                       0, s, hidden, m, hidden_size, chunks, xp);
+    st = OXR_LAUNCH_STATUS();
+    if (!st) st = launch_lm_head_wide(xp, (int)m, weight, hidden_size, vocab, logits, best, num_best, s);
+  } else if (lm_head_lds_supported(m, hidden_size)) {
     const int64_t num_tiles = (vocab + 15) / 16;
     num_best = (int)std::min<int64_t>(device_cus(), num_tiles);
     const int key = (m <= 16 ? 0 : 2) + (packed ? 1 : 0);
@@ -728,7 +972,8 @@ extern "C" int oxr_gemm_bf16_partial_packed(const oxr_bf16* x, int64_t ldx, int6
 
 extern "C" size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab) {
   if (m <= 0 || vocab <= 0) return 0;
-  return (size_t)((vocab + 15) / 16) * (size_t)m * sizeof(uint64_t);  // enough for 16-row tiles
+  const size_t tiles = (size_t)((vocab + 15) / 16) * (size_t)m * sizeof(uint64_t);  // enough for 16-row tiles
+  return m > 32 ? std::max(tiles, oxr::wide_workspace_bytes(m)) : tiles;
 }
 
 extern "C" int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size,

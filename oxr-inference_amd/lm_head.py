@@ -12,11 +12,13 @@ import torch
 from . import _lib
 from .gemm import PackedWeight, Weight
 
-MAX_ROWS = 64
+MAX_ROWS = 64          # token rows per launch with a row-major weight
+MAX_ROWS_PACKED = 256  # with a packed weight (up to 256 rows read the weight once)
 
 
 def workspace_bytes(rows: int, vocab: int) -> int:
-    return int(_lib.lib().oxr_lm_head_workspace_bytes(min(rows, MAX_ROWS), vocab))
+    """Workspace for ``rows`` token rows of either weight form (rows past one launch reuse it)."""
+    return int(_lib.lib().oxr_lm_head_workspace_bytes(min(rows, MAX_ROWS_PACKED), vocab))
 
 
 def lm_head_argmax(
@@ -41,8 +43,9 @@ def lm_head_argmax(
     need = workspace_bytes(n, vocab)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
-    for start in range(0, n, MAX_ROWS):
-        rows = min(MAX_ROWS, n - start)
+    step = MAX_ROWS_PACKED if packed else MAX_ROWS
+    for start in range(0, n, step):
+        rows = min(step, n - start)
         _lib.call(
             "oxr_lm_head_argmax_packed" if packed else "oxr_lm_head_argmax", hidden[start:].data_ptr(), rows,
             wt.data_ptr(), k, vocab,

@@ -251,6 +251,45 @@ def test_lm_head_config4_logits_and_argmax() -> None:
     assert np.array_equal(pred, oracle_lm_head.argmax(_bits(logits)))
 
 
+@pytest.mark.parametrize("rows", [256, 64, 40, 200])
+def test_lm_head_wide_rows_packed(rows) -> None:
+    """33..256 token rows with the packed weight: one launch reads the weight once (32x32x16
+    MFMA, token rows staged in LDS).  Config 4 at 256 rows, and row counts that leave partial
+    token tiles; logits within tolerance of the exact product, ids exact where the margin is clear
+    and always the first argmax of the kernel's own bf16 logits."""
+    g = torch.Generator(device="cuda").manual_seed(50 + rows)
+    hidden, weight = _rand(g, rows, 2048), _rand(g, 151_936, 2048, std=0.02)
+    packed = gemm.pack_weight(weight)
+    announce("lm head wide", rows)
+    pred, logits = lm_head.lm_head_argmax(hidden, packed, return_logits=True)
+    pred_only, _ = lm_head.lm_head_argmax(hidden, packed)
+    torch.cuda.synchronize()
+    exact = _exact(hidden, weight)
+    got = bf16.to_f32(_bits(logits)).astype(np.float64)
+    assert (np.abs(got - exact) <= ATOL + RTOL * np.abs(exact)).all()
+    ref_ids = oracle_lm_head.argmax(bf16.from_f32(exact.astype(np.float32)))
+    sure = oracle_lm_head.top2_margin(exact) > ATOL
+    pred = pred.cpu().numpy()
+    assert sure.mean() > 0.8
+    assert np.array_equal(pred[sure], ref_ids[sure])
+    assert np.array_equal(pred, oracle_lm_head.argmax(_bits(logits)))
+    assert np.array_equal(pred, pred_only.cpu().numpy())
+
+
+def test_lm_head_wide_ties_take_lowest_index() -> None:
+    g = torch.Generator(device="cuda").manual_seed(42)
+    vocab, k = 20_000, 1024
+    hidden, weight = _rand(g, 100, k), _rand(g, vocab, k, std=0.02)
+    top = (hidden[0].float() * 0.05).to(torch.bfloat16)
+    for v in (19_999, 8_000, 33, 7):  # different vocab tiles and workgroups: the lowest wins
+        weight[v] = top
+    announce("lm head wide ties")
+    pred, logits = lm_head.lm_head_argmax(hidden, gemm.pack_weight(weight), return_logits=True)
+    torch.cuda.synchronize()
+    assert int(pred[0]) == 7
+    assert np.array_equal(pred.cpu().numpy(), oracle_lm_head.argmax(_bits(logits)))
+
+
 def test_lm_head_ties_take_lowest_index() -> None:
     g = torch.Generator(device="cuda").manual_seed(41)
     vocab, k = 4096 + 32, 2048
