@@ -276,6 +276,13 @@ def time_configs(config, lm_weight, seed: int = 0) -> dict:
     us_a4 = _time_us(lambda: speculative.accept_batch(drafts4, dlen4, pred.view(64, 4)))
     wbytes = config.vocab_size * config.hidden_size * 2 + rows * config.hidden_size * 2
     flops = 2.0 * rows * config.hidden_size * config.vocab_size
+    # The verify step's own LM head (B = 8, S = 4: 32 rows), for its counters.
+    h32 = hidden[:32].contiguous()
+    pred32 = torch.empty(32, dtype=torch.int64, device=dev)
+    us_h32 = _time_us(lambda: lm_head.lm_head_argmax(h32, lm_weight, predicted=pred32, workspace=ws))
+    res["config5_lm_head_32_rows"] = {"us": us_h32, "bytes": config.vocab_size * config.hidden_size * 2,
+                                      "achieved": config.vocab_size * config.hidden_size * 2 / (us_h32 * 1e-6) / 1e9,
+                                      "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     res["config4_lm_head_accept"] = {
         "rows": rows, "lm_head_us": us_h, "accept_us": us_a4, "bytes": wbytes,
         "hbm_achieved": wbytes / (us_h * 1e-6) / 1e9, "hbm_frac": wbytes / (us_h * 1e-6) / 1e9 / HBM_PEAK_GBS,
@@ -389,6 +396,12 @@ def main() -> int:
         c = language.QWEN_SYNTHETIC
         w = gemm.pack_weight((torch.randn(c.vocab_size, c.hidden_size, device=device) * 0.02).to(torch.bfloat16))
         print(json.dumps(time_configs(c, w, args.seed)), flush=True)
+        # Five device copies of COPY_BYTES: the calibration workload of the FETCH_SIZE / WRITE_SIZE runs.
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
         return 0
     log("building workload")
     config, model, cache, table, histories, seq_lens, width = build_workload(args, device)
