@@ -587,6 +587,9 @@ __global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf1
         bf16_t* const bufs[4] = {xs0, xs1, xs2, xs3};
         xdma(xchunk(s + 2), bufs[(d + 2) & 3]);  // read at stage s - 2, before the last barrier
         __builtin_amdgcn_sched_barrier(0);
+        // This stage's weight chunk (loaded during stage s - 2) is in: the loads issued after it are stage
+        // s - 1's and this stage's token rows and stage s - 1's weights.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kXBlocksPerWave + 4));
         const bf16_t* xb = bufs[d & 3];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
