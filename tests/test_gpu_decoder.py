@@ -186,9 +186,9 @@ def test_chunked_extends_equal_full_sequence() -> None:
 def _loop_setup(seed, B=4, k=3, bs=16):
     rng = np.random.default_rng(seed)
     model, cpu_w = _model(SMALL, seed=seed)
-    num_blocks = 512
-    cache = _cache(SMALL, num_blocks, bs, seed=seed + 1)
     width = 40
+    num_blocks = max(512, B * width + 16)
+    cache = _cache(SMALL, num_blocks, bs, seed=seed + 1)
     ctx = rng.integers(100, 400, size=B).astype(np.int32)
     perm = rng.permutation(num_blocks).astype(np.int32)
     table = perm[: B * width].reshape(B, width)
@@ -199,8 +199,9 @@ def _loop_setup(seed, B=4, k=3, bs=16):
     return loop, model, cpu_w, cache, table, histories, ctx
 
 
-def test_verify_loop_graph_matches_oracle_steps() -> None:
-    loop, model, cpu_w, cache, table, histories, ctx = _loop_setup(5)
+@pytest.mark.parametrize("B", [4, 16])  # 16 sequences x 4 tokens: the 64-row LM head
+def test_verify_loop_graph_matches_oracle_steps(B) -> None:
+    loop, model, cpu_w, cache, table, histories, ctx = _loop_setup(5, B=B)
     B, k, s = loop.batch, loop.k, loop.tokens_per_seq
     announce("verify loop capture")
     loop.capture()
