@@ -64,6 +64,40 @@ __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
+// Exchanges between the lane groups of a wave on the vector ALU (no LDS round trip).  gfx950's
+// v_permlane16_swap / v_permlane32_swap give every lane {v[l], v[l ^ 16]} (resp. l ^ 32) as an
+// unordered pair, so a commutative combination of the two is exactly `v op shfl_xor(v, 16 | 32)`.
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v + v[lane ^ m] for m = 1, 2 (quad_perm), and for m = 4, 8 on values already equal within each
+// quad (resp. 8 lanes), where the half-row / row mirror supplies the same partner value: so
+// wave_sum gives the bits of the butterfly `for m = 1 .. 32: v += shfl_xor(v, m)`.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
+  v = dpp_add<0x141>(v);  // row_half_mirror (quad-uniform values): lane ^ 4
+  v = dpp_add<0x140>(v);  // row_mirror (8-lane-uniform values): lane ^ 8
+  return xor32_sum(xor16_sum(v));
+}
+
 __device__ __forceinline__ f32x4 mfma_16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                  0, 0);

@@ -76,8 +76,7 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(const bf16_t* __r
     ss += a * a;
     ss += b * b;
   }
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) ss += shfl_xor_f(ss, m);
+  ss = wave_sum(ss);  // the butterfly over lane ^ 1 .. 32, on the vector ALU
   if (threadIdx.x % kWave == 0) wave_ss[threadIdx.x / kWave] = ss;
   __syncthreads();
   ss = 0.f;

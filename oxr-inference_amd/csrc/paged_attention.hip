@@ -332,8 +332,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         if (t0 + 16 * (e >> 2) + 4 * g + (e & 3) > qpos) sv[e] = -INFINITY;
     }
     float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
+    mx = xor32_max(xor16_max(mx));
     // Probabilities exp2(s * c - m * c) against the running row maximum m;
     // the accumulators are rescaled only when some row's maximum moved (when
     // it did not, the factor is exactly 1).
@@ -396,8 +395,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   }
 
   // Merge each head's kStreams waves on chip.
-  float l_tot = l_run + shfl_xor_f(l_run, 16);
-  l_tot += shfl_xor_f(l_tot, 32);
+  const float l_tot = xor32_sum(xor16_sum(l_run));
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[dt];
   if (g == 0) {

@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
       for (int w2 = 8; w2 >= 1; w2 >>= 1)
 #pragma unroll
         for (int e = 0; e < w2; ++e) mt[e] = fmaxf(mt[e], mt[e + w2]);
-      const float mx = fmaxf(mt[0], shfl_xor_f(mt[0], 32));
+      const float mx = xor32_max(mt[0]);
       const bool moved = mx > m_run;
       if (__builtin_amdgcn_ballot_w64(moved)) {
         const float m_new = moved ? mx : m_run;
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   }
 
   // Normalise and store: lane (n, h) holds O^T[32dt + 8(e/4) + 4h + e%4][query n].
-  float l_tot = l_run + shfl_xor_f(l_run, 32);
+  const float l_tot = xor32_sum(l_run);
   if (qpos < len) {
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     bf16_t* dst = out + ((int64_t)(start + qpos) * H + head) * kVD + 4 * h;
