@@ -487,7 +487,10 @@ __global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(cons
 // workgroup per CU over the whole batch, but at least kMinSplitKeys keys of
 // the longest context per split.  (At B = 1, 256 workgroups would leave 64
 // keys each: the launch is then fixed cost, and the merge walks 64 partials.)
-constexpr int kMinSplitKeys = 256;
+#ifndef OXR_ATTN_MIN_SPLIT_KEYS
+#define OXR_ATTN_MIN_SPLIT_KEYS 256  // (overridable for measurement builds)
+#endif
+constexpr int kMinSplitKeys = OXR_ATTN_MIN_SPLIT_KEYS;
 int splits_for(int32_t batch, int32_t num_kv_heads, int hpw, int32_t max_seq_len) {
   const int64_t units = (int64_t)batch * (num_kv_heads / hpw);
   int64_t splits = (256 + units - 1) / units;
