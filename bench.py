@@ -1,6 +1,6 @@
 """Benchmark: the full HIP-graph speculative verify step on one MI355X.
 
-Workload (BASELINE config 5 at its headline point): a random-init 28-layer Qwen-style decoder
+Workload (the headline configuration, number 5 of the benchmark's configurations): a random-init 28-layer Qwen-style decoder
 (hidden 2048, 16 q / 8 kv heads, head_dim 128, q/k RMSNorm, SwiGLU 6144, vocab 151,936, bf16),
 B=8 sequences, k=3 drafts (S=4 verify tokens per sequence), KV length 4096 per sequence at the
 start, block size 16, pages drawn from a random permutation of the pool, histories of 1024
@@ -75,7 +75,10 @@ def build_workload(args, device):
     perm = rng.permutation(num_blocks).astype(np.int32)
     table = perm[: args.batch * width].reshape(args.batch, width)
     histories = [workloads.repetitive_history(rng, args.history, repetitive_tail=True) for _ in range(args.batch)]
-    seq_lens = np.full(args.batch, args.ctx, dtype=np.int32)
+    if args.ctx_min is None:
+        seq_lens = np.full(args.batch, args.ctx, dtype=np.int32)
+    else:  # configuration 5's mixed contexts: each sequence's context uniform in [ctx_min, ctx]
+        seq_lens = rng.integers(args.ctx_min, args.ctx + 1, size=args.batch).astype(np.int32)
     return config, model, cache, table, histories, seq_lens, width
 
 
@@ -229,7 +232,7 @@ def _time_us(fn, iters: int = 20, per_graph: int = 10) -> float:
 
 
 def time_configs(config, lm_weight, seed: int = 0) -> dict:
-    """The benchmark's per-kernel configurations (2 and 4) on the GPU path, inputs
+    """The benchmark's per-kernel configurations (the benchmark's configurations 1, 2 and 4) on the GPU path, inputs
     resident on the device.  Config 3 is the ``roofline`` launch and config 5 the step itself."""
     rng = np.random.default_rng(seed)
     dev = "cuda"
@@ -366,6 +369,8 @@ def main() -> int:
     p.add_argument("--batch", type=int, default=8)
     p.add_argument("--k", type=int, default=3)
     p.add_argument("--ctx", type=int, default=4096)
+    p.add_argument("--ctx-min", type=int, default=None,
+                   help="draw each sequence's context uniformly from [ctx-min, ctx] (default: all = ctx)")
     p.add_argument("--layers", type=int, default=28)
     p.add_argument("--history", type=int, default=1024)
     p.add_argument("--block-size", type=int, default=16)
@@ -378,6 +383,8 @@ def main() -> int:
     p.add_argument("--prefill-driver", action="store_true", help="only the prefill attention measurement")
     p.add_argument("--configs-driver", action="store_true", help="only the per-kernel configurations 1, 2 and 4")
     args = p.parse_args()
+    if args.ctx_min is not None and not 1 <= args.ctx_min <= args.ctx:
+        p.error("--ctx-min must be in [1, --ctx]")
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the verify step is "
@@ -469,7 +476,8 @@ def main() -> int:
         "data": "synthetic (random-init weights, random context K/V, repetitive table-like histories)",
         "config": {
             "workload": "full hipGraph verify step (BASELINE config 5)", "batch": args.batch, "k": args.k,
-            "tokens_per_seq": s, "ctx_start": args.ctx, "layers": config.num_layers, "hidden": config.hidden_size,
+            "tokens_per_seq": s, "ctx_start": args.ctx if args.ctx_min is None else f"uniform {args.ctx_min}-{args.ctx}",
+            "layers": config.num_layers, "hidden": config.hidden_size,
             "heads": f"{config.num_heads}/{config.num_kv_heads}", "head_dim": config.head_dim,
             "intermediate": config.intermediate_size, "vocab": config.vocab_size, "block_size": args.block_size,
             "history": args.history, "max_n": args.max_n,
