@@ -105,6 +105,9 @@ int launch(const bf16_t* x, int64_t ldx, const int64_t* ids, int64_t vocab, cons
   else if (MODE == kAddPartials && k_splits == 4)
     hipLaunchKernelGGL((rms_norm_kernel<MODE, 4>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
                        w, eps, residual, out, ldo, out_packed);
+  else if (MODE == kAddPartials && k_splits == 8)
+    hipLaunchKernelGGL((rms_norm_kernel<MODE, 8>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
+                       w, eps, residual, out, ldo, out_packed);
   else
     hipLaunchKernelGGL((rms_norm_kernel<MODE, 0>), grid, block, 0, s, x, ldx, ids, vocab, partials, k_splits, rows, D,
                        w, eps, residual, out, ldo, out_packed);
