@@ -173,10 +173,10 @@ def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
             "achieved_gbs": traffic / (us * 1e-6) / 1e9}
 
 
-def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, seed: int = 0) -> dict:
-    """Prefill attention (``attention.varlen``, the drop-in for attention.py:47-59): causal over
-    ``seqs`` sequences of ``length`` tokens at the model's head shape, inputs resident on the device.
-    Flops = 4 * head_dim * heads * (causal query-key pairs)."""
+def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, seed: int = 0, causal: bool = True) -> dict:
+    """Prefill attention (``attention.varlen``, the drop-in for attention.py:47-59): causal or
+    bidirectional over ``seqs`` sequences of ``length`` tokens at the model's head shape, inputs
+    resident on the device.  Flops = 4 * head_dim * heads * (query-key pairs attended)."""
     h, kv, d = config.num_heads, config.num_kv_heads, config.head_dim
     t = seqs * length
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -186,20 +186,20 @@ def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, see
     cu = torch.arange(0, t + 1, length, dtype=torch.int32, device="cuda")
     out = torch.empty_like(q)
     for _ in range(3):
-        attention.varlen(q, k, v, cu, length, causal=True, out=out)
+        attention.varlen(q, k, v, cu, length, causal=causal, out=out)
     stream = torch.cuda.current_stream()  # where the wrapper launches
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
     for _ in range(iters):
-        attention.varlen(q, k, v, cu, length, causal=True, out=out)
+        attention.varlen(q, k, v, cu, length, causal=causal, out=out)
     end.record(stream)
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1000.0 / iters
-    flops = 4.0 * d * h * seqs * (length * (length + 1) / 2)
+    flops = 4.0 * d * h * seqs * (length * (length + 1) / 2 if causal else length * length)
     tflops = flops / (us * 1e-6) / 1e12
     del q, k, v, out
-    return {"workload": f"varlen causal, {seqs} x {length} tokens, {h}/{kv} heads, head_dim {d}", "us": us,
+    return {"workload": f"varlen {'causal' if causal else 'bidirectional'}, {seqs} x {length} tokens, {h}/{kv} heads, head_dim {d}", "us": us,
             "flops": flops, "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
 
@@ -398,6 +398,7 @@ def main() -> int:
 
     if args.prefill_driver:
         print(json.dumps(time_prefill(language.QWEN_SYNTHETIC)), flush=True)
+        print(json.dumps(time_prefill(language.QWEN_SYNTHETIC, causal=False)), flush=True)
         return 0
     if args.configs_driver:
         c = language.QWEN_SYNTHETIC
@@ -451,6 +452,7 @@ def main() -> int:
     decode = time_decode(config, model, cache, loop)
     log(f"decode step (B={decode['batch']}, one token each) {decode['step_us']:.1f} us")
     prefill = time_prefill(config)
+    prefill_bidir = time_prefill(config, causal=False)
     log(f"prefill attention {prefill['us']:.1f} us, {prefill['achieved']:.0f} TFLOP/s")
     configs = time_configs(config, model.weights.lm_head, args.seed)
     log("configs: " + json.dumps(configs))
@@ -496,6 +498,7 @@ def main() -> int:
                         "achieved": decode["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": decode["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill_attention": prefill,
+        "prefill_attention_bidirectional": prefill_bidir,
         "configs": configs,
         "cpu_baseline": cpu,
         "wall_s_timed": wall,

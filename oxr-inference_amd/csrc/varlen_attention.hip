@@ -34,6 +34,10 @@
 //   row's diagonal are masked per element; keys past the sequence are masked.
 #include "common.h"
 
+#ifndef OXR_VARLEN_PINGPONG
+#define OXR_VARLEN_PINGPONG 1  // 0: the 4-wave kernel (for measurement builds)
+#endif
+
 namespace oxr {
 namespace {
 
@@ -272,6 +276,271 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   }
 }
 
+// Ping-pong form: a workgroup of 8 waves covers 256 query rows; waves w and w + 4 run on the same
+// SIMD.  Group A (waves 0-3) and group B (waves 4-7) alternate between a vector phase (the online
+// softmax of a tile's scores) and a matrix phase (PV of that tile, QK^T of the next), in opposite
+// phases, with a workgroup barrier between phases, so each SIMD has one wave issuing exponentials
+// while the other issues MFMAs.  Phases, for tile t:
+//   phase 2t + 1: loads of V(t + 1) and K(t + 2) start; A: PV(t), QK(t + 1); B: softmax(t)
+//   phase 2t + 2: A: softmax(t + 1); B: PV(t), QK(t + 1); then every wave waits for its loads
+// so V(t) and K(t + 1) are read in phases 2t + 1 and 2t + 2 and their buffers are refilled at the
+// start of phase 2t + 3, after both reads.
+constexpr int kPWaves = 8;
+constexpr int kPRows = 32 * kPWaves;  // query rows per workgroup
+constexpr int kPLoadsPerWave = kKeyTile * kVD * 2 / 1024 / kPWaves;
+
+template <bool kCausal>
+__global__ __launch_bounds__(64 * kPWaves, 1) void varlen_attention_pp_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const int32_t* __restrict__ cu_seqlens, int H, int KV, int num_qtiles, float scale_log2,
+    bf16_t* __restrict__ out) {
+  __shared__ bf16_t s_k0[kKeyTile * kVD], s_k1[kKeyTile * kVD];
+  __shared__ bf16_t s_v0[kKeyTile * kVD], s_v1[kKeyTile * kVD];
+
+  // Work item order as in varlen_attention_kernel (XCD-contiguous items, late query tiles first).
+  const int total = (int)gridDim.x, xcd = (int)blockIdx.x & 7, slot = (int)blockIdx.x >> 3;
+  const int w = xcd * (total >> 3) + min(xcd, total & 7) + slot;
+  const int pair = w / num_qtiles;
+  const int seq = pair / KV, kvh = pair - seq * KV;
+  const int start = cu_seqlens[seq], len = cu_seqlens[seq + 1] - start;
+  const int G = H / KV, rph = kPRows / G;
+  const int q0 = (num_qtiles - 1 - (w - pair * num_qtiles)) * rph;
+  if (q0 >= len) return;  // whole workgroup: before any barrier
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool group_a = wave < kPWaves / 2;
+  const int n = lane & 31, h = lane >> 5;
+  const int rho = 32 * wave + n;
+  const int head = kvh * G + rho / rph;
+  const int qpos = q0 + rho % rph;
+  const int first_off = rph >= 32 ? (32 * wave) % rph : 0;
+  const int wave_first = q0 + first_off;
+  const int wave_last = kCausal ? min(wave_first + min(rph, 32) - 1, len - 1) : len - 1;
+
+  u32x4 qf[8];
+  {
+    const int qrow = min(qpos, len - 1);
+    const bf16_t* src = q + ((int64_t)(start + qrow) * H + head) * kVD + 8 * h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qf[i] = ld128(src + 16 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(qf[i]));
+
+  const int key_end = kCausal ? min(len, q0 + rph) : len;
+  const int tiles = (key_end + kKeyTile - 1) / kKeyTile;
+
+  // Direct-to-LDS tile loads, rotated rows as in varlen_attention_kernel; kPLoadsPerWave 1 KiB
+  // blocks per wave and tensor.
+  auto dma = [&](const bf16_t* src, int t, bf16_t* dst, int rot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kPLoadsPerWave; ++u) {
+      const int j = kPLoadsPerWave * wave + u;
+      const int row = 4 * j + (lane >> 4), pos = lane & 15;
+      const int key = min(t * kKeyTile + row, len - 1);
+      const int64_t base = ((int64_t)(start + key) * KV + kvh) * kVD;
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(src + base + 8 * ((pos - rot * row) & 15)),
+          (void __attribute__((address_space(3)))*)(dst + 512 * j), 16, 0, 0);
+    }
+  };
+
+  float m_run = -INFINITY, mc_run = 0.f, l_run = 0.f;
+  f32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  const int tr_key = 4 * h + ((lane & 15) >> 2);
+  int tr_off[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+    tr_off[dt] = 8 * ((4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1) + 4 * tr_key) & 15) + 4 * (lane & 1);
+
+  f32x16 sv[2];  // scores of the tile whose softmax is next
+  u32x4 pb[4];   // P^T of the tile whose PV is next
+  // A tile is skipped by a wave when all of its keys are past the wave's last row (wave-uniform).
+  auto live = [&](int t) __attribute__((always_inline)) { return t >= 0 && t < tiles && t * kKeyTile <= wave_last; };
+
+  // Matrix phase of tile t: PV(t) from vb (V(t)), then QK^T of tile t + 1 from kb (K(t + 1)).  The
+  // LDS fragments are read one step ahead of their products (one step: a V key step, a K dim step),
+  // with a scheduling barrier per step: left alone, the compiler issues all 48 reads first and needs
+  // 128 more registers than the wave has.
+  auto vread = [&](const bf16_t* vb, int ks, u32x2 (&d)[4][2]) __attribute__((always_inline)) {
+    const bf16_t* vrow = vb + (16 * ks + tr_key) * kVD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      d[dt][0] = lds_read_tr16(vrow + tr_off[dt]);            // keys 16ks + 4h + (0..3)
+      d[dt][1] = lds_read_tr16(vrow + 8 * kVD + tr_off[dt]);  // keys 16ks + 8 + 4h + (0..3)
+    }
+  };
+  auto kread = [&](const bf16_t* kb_, int i, u32x4 (&d)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      d[kb] = *reinterpret_cast<const u32x4*>(kb_ + (32 * kb + n) * kVD + 8 * ((2 * i + h + n) & 15));
+  };
+  auto matrix_phase = [&](int t, const bf16_t* kb, const bf16_t* vb) __attribute__((always_inline)) {
+    const bool pv = live(t), next = live(t + 1);
+    u32x4 kr[2][2];
+    if (pv) {
+      u32x2 vr[2][4][2];
+      vread(vb, 0, vr[0]);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < 3) vread(vb, ks + 1, vr[(ks + 1) & 1]);
+        else if (next) {
+          kread(kb, 0, kr[0]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const u32x2 lo = vr[ks & 1][dt][0], hi = vr[ks & 1][dt][1];
+          o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[ks], o[dt]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if (next) {
+      kread(kb, 0, kr[0]);
+    }
+    if (next) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sv[kb2][e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i + 1 < 8) kread(kb, i + 1, kr[(i + 1) & 1]);
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) sv[kb2] = mfma_32x32x16(kr[i & 1][kb2], qf[i], sv[kb2]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // Vector phase of tile t: mask, online softmax, P^T packed for the next matrix phase.
+  auto vector_phase = [&](int t) __attribute__((always_inline)) {
+    if (!live(t)) return;
+    const int kt0 = t * kKeyTile;
+    const bool edge = (kCausal && kt0 + kKeyTile - 1 > wave_first) || kt0 + kKeyTile > len;
+    if (edge) {
+      // Key kt0 + 4h + c with c = 32kb + 8(e / 4) + e % 4 a constant: compared against two per-tile
+      // limits, so no per-element lane offsets are kept in registers across tiles.
+      const int lim_len = len - kt0 - 4 * h, lim_q = qpos - kt0 - 4 * h;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int c = 32 * kb + 8 * (e >> 2) + (e & 3);
+          if (c >= lim_len || (kCausal && c > lim_q)) sv[kb][e] = -INFINITY;
+        }
+    }
+    float mt[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mt[e] = fmaxf(sv[0][e], sv[1][e]);
+#pragma unroll
+    for (int w2 = 8; w2 >= 1; w2 >>= 1)
+#pragma unroll
+      for (int e = 0; e < w2; ++e) mt[e] = fmaxf(mt[e], mt[e + w2]);
+    const float mx = xor32_max(mt[0]);
+    const bool moved = mx > m_run;
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+      const float m_new = moved ? mx : m_run;
+      const float mc_new = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+      const float alpha = !moved ? 1.0f : (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc_run - mc_new));
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      m_run = m_new;
+      mc_run = mc_new;
+    }
+    float ps[16];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[ks >> 1][8 * (ks & 1) + e], scale_log2, -mc_run));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ps[4 * ks + e] = pv[e] + pv[e + 4];
+      pb[ks] = u32x4{pack_bf_hw(pv[0], pv[1]), pack_bf_hw(pv[2], pv[3]), pack_bf_hw(pv[4], pv[5]),
+                     pack_bf_hw(pv[6], pv[7])};
+    }
+#pragma unroll
+    for (int w2 = 8; w2 >= 1; w2 >>= 1)
+#pragma unroll
+      for (int e = 0; e < w2; ++e) ps[e] += ps[e + w2];
+    l_run += ps[0];
+  };
+  // The barrier between phases orders LDS reads before the refills of later phases; its memory
+  // clobber keeps LDS accesses on their side.  Only the end of an even phase waits for this wave's
+  // tile loads (a fence or __syncthreads would wait for them at every barrier).
+  auto phase_end = [&](bool wait_loads) __attribute__((always_inline)) {
+    if (wait_loads) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+  };
+  // Phase 2t + 1 and phase 2t + 2, with the buffers named statically: K(t + 1) in kb, V(t) in vb,
+  // and the loads of K(t + 2) into kd, V(t + 1) into vd.  Each group runs its own loop (its phases in
+  // its own order), so the register allocator sees one straight sequence per group; both loops pass
+  // the same barriers, two per tile.
+  auto loads = [&](int t, bf16_t* kd, bf16_t* vd) __attribute__((always_inline)) {
+    if (t + 1 < tiles) dma(v, t + 1, vd, 4);
+    if (t + 2 < tiles) dma(k, t + 2, kd, 1);
+  };
+  auto iteration_a = [&](int t, const bf16_t* kb, const bf16_t* vb, bf16_t* kd, bf16_t* vd)
+                         __attribute__((always_inline)) {
+    loads(t, kd, vd);
+    matrix_phase(t, kb, vb);
+    phase_end(false);
+    vector_phase(t + 1);
+    phase_end(true);
+  };
+  auto iteration_b = [&](int t, const bf16_t* kb, const bf16_t* vb, bf16_t* kd, bf16_t* vd)
+                         __attribute__((always_inline)) {
+    loads(t, kd, vd);
+    vector_phase(t);
+    phase_end(false);
+    matrix_phase(t, kb, vb);
+    phase_end(true);
+  };
+
+  // Prologue: K(0) in; phase -1 (A: QK(0); V(0) and K(1) start loading); phase 0 (A: softmax(0);
+  // B: QK(0)).
+  dma(k, 0, s_k0, 1);
+  phase_end(true);
+  if (0 < tiles) dma(v, 0, s_v0, 4);
+  if (1 < tiles) dma(k, 1, s_k1, 1);
+  if (group_a) {
+    matrix_phase(-1, s_k0, s_v0);  // QK(0) only
+    phase_end(false);
+    vector_phase(0);
+    phase_end(true);
+    for (int t = 0; t < tiles; t += 2) {
+      iteration_a(t, s_k1, s_v0, s_k0, s_v1);
+      if (t + 1 < tiles) iteration_a(t + 1, s_k0, s_v1, s_k1, s_v0);
+    }
+  } else {
+    phase_end(false);
+    matrix_phase(-1, s_k0, s_v0);
+    phase_end(true);
+    for (int t = 0; t < tiles; t += 2) {
+      iteration_b(t, s_k1, s_v0, s_k0, s_v1);
+      if (t + 1 < tiles) iteration_b(t + 1, s_k0, s_v1, s_k1, s_v0);
+    }
+  }
+
+  const float l_tot = xor32_sum(l_run);
+  if (qpos < len) {
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    bf16_t* dst = out + ((int64_t)(start + qpos) * H + head) * kVD + 4 * h;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * m) =
+            u32x2{pack_bf(o[dt][4 * m] * inv, o[dt][4 * m + 1] * inv),
+                  pack_bf(o[dt][4 * m + 2] * inv, o[dt][4 * m + 3] * inv)};
+  }
+}
+
 }  // namespace
 }  // namespace oxr
 
@@ -288,13 +557,19 @@ extern "C" int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const 
   OXR_RETURN_IF(!q || !k || !v || !cu_seqlens || !out, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 != 0 || (uintptr_t)out % 8 != 0,
                 OXR_ERR_UNSUPPORTED);
-  const int rows_per_head = kVRows / G;
+  // Bidirectional prefill runs the ping-pong kernel; the causal form of that kernel needs more
+  // registers than two waves per SIMD have (it spills), so causal prefill runs the 4-wave kernel.
+  const bool pingpong = OXR_VARLEN_PINGPONG != 0 && !causal;
+  const int rows_per_head = (pingpong ? kPRows : kVRows) / G;
   const int num_qtiles = (max_len + rows_per_head - 1) / rows_per_head;
   OXR_RETURN_IF((int64_t)num_qtiles * num_kv_heads * num_seqs > INT32_MAX, OXR_ERR_UNSUPPORTED);
   const dim3 grid((unsigned)(num_qtiles * num_kv_heads * num_seqs));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
-  if (causal)
+  if (pingpong)
+    hipLaunchKernelGGL(varlen_attention_pp_kernel<false>, grid, dim3(64 * kPWaves), 0, s, q, k, v, cu_seqlens,
+                       num_heads, num_kv_heads, num_qtiles, scale_log2, out);
+  else if (causal)
     hipLaunchKernelGGL(varlen_attention_kernel<true>, grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
                        num_heads, num_kv_heads, num_qtiles, scale_log2, out);
   else

@@ -49,9 +49,10 @@ def test_tile_edges_and_empty(causal) -> None:
     _case([1, 15, 16, 17, 0, 63, 64, 65, 127, 128, 129, 200], 16, 8, causal, seed=1 + causal)
 
 
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("kv", [16, 8, 4, 2])
-def test_head_groupings(kv) -> None:
-    _case([97, 300, 1], 16, kv, True, seed=10 + kv)
+def test_head_groupings(kv, causal) -> None:
+    _case([97, 300, 1], 16, kv, causal, seed=10 + kv)
 
 
 @pytest.mark.parametrize("causal", [True, False])
