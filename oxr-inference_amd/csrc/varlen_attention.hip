@@ -32,6 +32,9 @@
 //   wave overlap.
 // * Causal: key tiles above a wave's last row are skipped, tiles that cross a
 //   row's diagonal are masked per element; keys past the sequence are masked.
+// Causal prefill runs this 4-wave kernel.  Bidirectional prefill runs the
+// 8-wave ping-pong kernel further down (same tiles and products, its two wave
+// groups alternating softmax and MFMA phases on each SIMD).
 #include "common.h"
 
 #ifndef OXR_VARLEN_PINGPONG
