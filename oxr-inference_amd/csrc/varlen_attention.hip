@@ -67,6 +67,20 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const bf16_t* p) {
   return __builtin_bit_cast(u32x2, x);
 }
 
+// Maximum of the 32 scores of a lane, as three-input maxima (each a v_max3_f32).
+__device__ __forceinline__ float row_max32(const f32x16 (&sv)[2]) {
+  float a[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    const int x = 3 * i, y = 3 * i + 1, z = 3 * i + 2;
+    a[i] = fmaxf(fmaxf(sv[x >> 4][x & 15], sv[y >> 4][y & 15]), sv[z >> 4][z & 15]);
+  }
+  a[10] = fmaxf(sv[1][14], sv[1][15]);
+  const float b0 = fmaxf(fmaxf(a[0], a[1]), a[2]), b1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
+  const float b2 = fmaxf(fmaxf(a[6], a[7]), a[8]), b3 = fmaxf(a[9], a[10]);
+  return fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
+}
+
 template <bool kCausal>
 __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -194,15 +208,9 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
             if (key >= len || (kCausal && key > qpos)) cur[kb][e] = -INFINITY;
           }
       }
-      // Row maximum as a tree (max is exact in any order).
-      float mt[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mt[e] = fmaxf(cur[0][e], cur[1][e]);
-#pragma unroll
-      for (int w2 = 8; w2 >= 1; w2 >>= 1)
-#pragma unroll
-        for (int e = 0; e < w2; ++e) mt[e] = fmaxf(mt[e], mt[e + w2]);
-      const float mx = xor32_max(mt[0]);
+      // Row maximum (exact in any order) as a tree of three-input maxima (v_max3_f32): 32 scores in
+      // 16 instructions instead of 31.
+      const float mx = xor32_max(row_max32(cur));
       const bool moved = mx > m_run;
       if (__builtin_amdgcn_ballot_w64(moved)) {
         const float m_new = moved ? mx : m_run;
@@ -436,14 +444,7 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void varlen_attention_pp_kernel(
           if (c >= lim_len || (kCausal && c > lim_q)) sv[kb][e] = -INFINITY;
         }
     }
-    float mt[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) mt[e] = fmaxf(sv[0][e], sv[1][e]);
-#pragma unroll
-    for (int w2 = 8; w2 >= 1; w2 >>= 1)
-#pragma unroll
-      for (int e = 0; e < w2; ++e) mt[e] = fmaxf(mt[e], mt[e + w2]);
-    const float mx = xor32_max(mt[0]);
+    const float mx = xor32_max(row_max32(sv));
     const bool moved = mx > m_run;
     if (__builtin_amdgcn_ballot_w64(moved)) {
       const float m_new = moved ? mx : m_run;
