@@ -52,6 +52,12 @@ constexpr uint32_t kBf16One = 0x3f80u;
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+#ifndef OXR_NT_KV
+#define OXR_NT_KV 0  // 1: context K/V through non-temporal loads (measurement builds)
+#endif
+// Context K/V rows: read once per layer and step.
+__device__ __forceinline__ u32x4 ld_kv(const void* p) { return OXR_NT_KV ? ld128_nt(p) : ld128(p); }
+
 struct PairRegs {
   u32x4 k[2][4];  // tile p: K[key 16p + r][32i + 8g .. +7], i = 0..3
   u32x4 v[2][4];  // tile p: V[key 16p + r][32c + 8g .. +7], c = 0..3
@@ -85,9 +91,9 @@ __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict
     const bf16_t* ks = k_cache + page + off + 8 * g;
     const bf16_t* vs = v_cache + page + off + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld128(ks + 32 * i);
+    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld_kv(ks + 32 * i);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) pr.v[p][c] = ld128(vs + 32 * c);
+    for (int c = 0; c < 4; ++c) pr.v[p][c] = ld_kv(vs + 32 * c);
   }
 }
 
