@@ -85,6 +85,9 @@ struct GemmArgs {
   float* part;      // kPartial: [k_splits, M, N]
 };
 
+#ifndef OXR_NT_PART
+#define OXR_NT_PART 0  // 1: k-split partials stored non-temporally (measurement builds)
+#endif
 #ifndef OXR_NT_W
 #define OXR_NT_W 1  // 0: weights through ordinary loads (measurement builds)
 #endif
@@ -252,7 +255,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
         const int64_t col0 = n0 + 16 * a + 4 * g;
         float* dst = args.part + ((int64_t)blockIdx.y * args.M + tok) * args.N + col0;
         if (col0 + 3 < args.N) {
-          *reinterpret_cast<f32x4*>(dst) = acc[a][bt];
+          if (OXR_NT_PART) __builtin_nontemporal_store(acc[a][bt], reinterpret_cast<f32x4*>(dst));
+          else *reinterpret_cast<f32x4*>(dst) = acc[a][bt];
         } else {
           for (int j = 0; j < 4; ++j)
             if (col0 + j < args.N) dst[j] = acc[a][bt][j];

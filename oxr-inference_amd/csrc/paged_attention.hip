@@ -52,6 +52,9 @@ constexpr uint32_t kBf16One = 0x3f80u;
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+#ifndef OXR_NT_PART
+#define OXR_NT_PART 0  // 1: split partials stored non-temporally (measurement builds)
+#endif
 #ifndef OXR_NT_KV
 #define OXR_NT_KV 0  // 1: context K/V through non-temporal loads (measurement builds)
 #endif
@@ -433,7 +436,9 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
       dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
       dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
     } else {
-      *reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kRows + rr) * kD + d0) = acc;
+      f32x4* const po = reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kRows + rr) * kD + d0);
+      if (OXR_NT_PART) __builtin_nontemporal_store(acc, po);
+      else *po = acc;
       if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + ((unit0 + split) * kRows + rr) * 2) = f32x2{mmax, l};
     }
   }
