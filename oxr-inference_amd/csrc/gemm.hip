@@ -807,6 +807,9 @@ int dispatch(const GemmArgs& a, const LaunchConfig& c, Layout layout, hipStream_
 // at most 8 steps of 128 (o_proj: 1 wave; qkv, gate_up, down_proj: 2).  More
 // waves per workgroup only add requests in flight to an already saturated
 // memory pipeline (4 waves: gate_up 18.1 vs 15.7 us, down_proj 9.9 vs 8.5).
+#ifndef OXR_GEMM_WAVE_STEPS
+#define OXR_GEMM_WAVE_STEPS 8  // most 128-k steps per wave before a GEMM adds waves (measurement builds)
+#endif
 #ifndef OXR_GEMM_NA2_TILES
 #define OXR_GEMM_NA2_TILES 160  // 32-row tiles from which a whole-K GEMM takes two tiles per workgroup
 #endif
@@ -824,7 +827,8 @@ LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
     c.na = (n_rows + 31) / 32 >= OXR_GEMM_NA2_TILES ? 2 : 1;
   }
   const int64_t k_slice = K / c.k_splits;
-  while (k_slice / c.waves > 8 * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 8) c.waves *= 2;
+  while (k_slice / c.waves > OXR_GEMM_WAVE_STEPS * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 8)
+    c.waves *= 2;
   return c;
 }
 
