@@ -776,7 +776,6 @@ int dispatch_waves(const GemmArgs& a, const LaunchConfig& c, hipStream_t s) {
     case 1: return dispatch_nb<NA, EPI, 1, PW, PX>(a, c, s);
     case 2: return dispatch_nb<NA, EPI, 2, PW, PX>(a, c, s);
     case 4: return dispatch_nb<NA, EPI, 4, PW, PX>(a, c, s);
-    case 8: return dispatch_nb<NA, EPI, 8, PW, PX>(a, c, s);
     default: return OXR_ERR_UNSUPPORTED;
   }
 }
@@ -827,7 +826,9 @@ LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
     c.na = (n_rows + 31) / 32 >= OXR_GEMM_NA2_TILES ? 2 : 1;
   }
   const int64_t k_slice = K / c.k_splits;
-  while (k_slice / c.waves > OXR_GEMM_WAVE_STEPS * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 8)
+  // At most 4 waves: an 8-wave workgroup has 256 registers per wave, and its 3- and 4-tile token
+  // forms spill (up to 1.1 KiB per lane).
+  while (k_slice / c.waves > OXR_GEMM_WAVE_STEPS * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 4)
     c.waves *= 2;
   return c;
 }
