@@ -114,7 +114,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
   const int64_t K = args.K;
   const int64_t k_slice = K / gridDim.y;
   const int64_t k_per_wave = k_slice / WAVES;
-  const int64_t k_begin = blockIdx.y * k_slice + wave * k_per_wave, k_end = k_begin + k_per_wave;
+  const int64_t k_begin = blockIdx.y * k_slice + wave * k_per_wave;  // this wave walks [k_begin, k_begin + k_per_wave)
 
   // Weight pointers of this lane, one per loaded tile (rows past N clamp to
   // the last row, or tile, whose results are dropped).  Packed: the lane's
