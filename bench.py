@@ -154,7 +154,7 @@ def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
     slots = [int(table[i, p // bs]) * bs + p % bs for i, p in enumerate(positions)]
     tables = [table[i, : (p + 1 + bs - 1) // bs].tolist() for i, p in enumerate(positions)]
     graphs.run([1] * b, positions, slots, (seq + 1).tolist(), tables)
-    graph = graphs._graphs[graphs.buckets[-1]][0]
+    graph = graphs.graph(graphs.buckets[-1])
     for _ in range(3):
         graph.replay()
     stream = torch.cuda.current_stream()  # where replay() launches the graph
@@ -238,14 +238,32 @@ def time_configs(config, lm_weight, seed: int = 0) -> dict:
     dev = "cuda"
     res = {}
 
-    # Config 1: drafting (max_n 3, k 3) over 4 histories of 512 tokens, then acceptance.
+    # Config 1: drafting (max_n 3, k 3) over 4 histories of 512 tokens, argmax of the fp32 verify
+    # logits [4, 4, V] with the drafts planted (p = 0.6), then acceptance.
     hist = torch.from_numpy(workloads.drafting_histories(seed, 4, 512)).to(dev)
     hlen = torch.full((4,), 512, dtype=torch.int32, device=dev)
     draft, dlen = speculative.propose_batch(hist, hlen, 3, max_n=3)
-    predicted = torch.from_numpy(rng.integers(0, config.vocab_size, size=(4, 4))).to(dev)
+    logits = torch.from_numpy(workloads.plant_logits(rng, draft.cpu().numpy(), dlen.cpu().numpy(), 4,
+                                                     config.vocab_size)).to(dev)
+    predicted = torch.empty(4, 4, dtype=torch.int64, device=dev)
+    aws = torch.empty(max(int(lm_head._lib.lib().oxr_argmax_workspace_bytes(16, config.vocab_size)), 1),
+                      dtype=torch.uint8, device=dev)
+
+    def config1_step():
+        speculative.propose_batch(hist, hlen, 3, max_n=3, draft=draft, draft_len=dlen)
+        lm_head.argmax(logits, out=predicted, workspace=aws)
+        speculative.accept_batch(draft, dlen, predicted)
+
     us_d = _time_us(lambda: speculative.propose_batch(hist, hlen, 3, max_n=3, draft=draft, draft_len=dlen))
+    us_m = _time_us(lambda: lm_head.argmax(logits, out=predicted, workspace=aws))
     us_a = _time_us(lambda: speculative.accept_batch(draft, dlen, predicted))
-    res["config1_draft_accept"] = {"draft_us": us_d, "accept_us": us_a, "batch": 4, "history": 512, "max_n": 3, "k": 3}
+    us_step = _time_us(config1_step)
+    unit = 4 * 512 * 4 + logits.numel() * 4  # history + fp32 logits, each read once
+    res["config1_draft_argmax_accept"] = {
+        "step_us": us_step, "draft_us": us_d, "argmax_us": us_m, "accept_us": us_a, "bytes": unit,
+        "achieved": unit / (us_step * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": unit / (us_step * 1e-6) / 1e9 / HBM_PEAK_GBS, "batch": 4, "history": 512, "max_n": 3, "k": 3,
+        "accepted": int(speculative.accept_batch(draft, dlen, predicted).accepted.sum().item())}
 
     # Config 2: fused q/k RMSNorm + RoPE + paged KV write, 32 sequences x 4 tokens, 65,536-block pool.
     t, h, kv, d = 128, config.num_heads, config.num_kv_heads, config.head_dim
@@ -337,8 +355,8 @@ def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict
     times, committed = [], []
     for i in range(args.cpu_warmup + args.cpu_steps):
         t0 = time.perf_counter()
-        _, _, taken, _ = oracle_decoder.verify_step(config, weights, hist, seq_lens, ctable, args.k, args.max_n, ck, cv,
-                                                    args.block_size)
+        taken = oracle_decoder.verify_step(config, weights, hist, seq_lens, ctable, args.k, args.max_n, ck, cv,
+                                           args.block_size).taken
         dt = time.perf_counter() - t0
         if i >= args.cpu_warmup:
             times.append(dt)

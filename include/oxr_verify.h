@@ -68,17 +68,42 @@ int oxr_ngram_propose(const int32_t* history, int64_t history_stride, const int3
  *   ids[b*S + j]       = j == 0 ? history[b, L-1] : (j-1 < draft_len ? draft[j-1] : 0)
  *   positions[b*S + j] = seq_len[b] + j
  *   slots[b*S + j]     = block_table[b, pos / block_size] * block_size + pos % block_size
- *                        (-1 when pos / block_size >= table_stride)
+ *                        (-1 when pos / block_size >= table_stride or the table entry is negative)
  *   attn_seq_lens[b]   = seq_len[b] + S
  * seq_len is the KV length before the step (the reference's seq.length).
+ * Drafts are further capped by the room engine.py:683-684 leaves:
+ * k_b <= max_tokens[b] - L - 1 (when max_tokens is non-null) and
+ * k_b <= max_positions - seq_len[b] - 1 (when max_positions > 0).
  * tokens_per_seq (S) must be >= k + 1.  ids/positions/slots are int64 [B*S].
  */
 int oxr_propose_verify_inputs(const int32_t* history, int64_t history_stride, const int32_t* history_len,
                               int32_t batch, int32_t max_n, int32_t k, const int32_t* k_limit,
                               const int32_t* seq_len, const int32_t* block_table, int64_t table_stride,
-                              int32_t block_size, int32_t tokens_per_seq, int32_t* draft, int32_t* draft_len,
-                              int64_t* ids, int64_t* positions, int64_t* slots, int32_t* attn_seq_lens,
-                              oxr_stream_t stream);
+                              int32_t block_size, int32_t tokens_per_seq, const int32_t* max_tokens,
+                              int32_t max_positions, int32_t* draft, int32_t* draft_len, int64_t* ids,
+                              int64_t* positions, int64_t* slots, int32_t* attn_seq_lens, oxr_stream_t stream);
+
+/*
+ * Step inputs of the list-interface graph runners, expanded on the device.
+ * Replaces the host-side padding, scratch-page filling and pack_page_table of
+ * DecodeGraphs.run / ExtendGraphs.run (oxr_runtime/decode_graph.py:92-119,
+ * 176-205; kv_cache.py:60-72): the host writes one int64 record for up to
+ * `capacity` sequences of tokens_per_seq (S) rows each --
+ *   [n, P, ids[capacity*S], positions[capacity*S], slots[capacity*S],
+ *    seq_lens[capacity], page offsets[capacity + 1], pages[P]]
+ * (rows of the n real sequences; sequence b's pages are
+ * pages[off[b] .. off[b+1])) -- copies it in one transfer, and this kernel
+ * fills the bucket's tensors: ids / positions / slots int64 [bucket*S],
+ * seq_lens int32 [bucket], table int32 [bucket, width].  Sequences b >= n
+ * become scratch rows (id 0, position j, slot scratch_block*block_size + j,
+ * seq_len S); table entries past a sequence's pages hold scratch_block.
+ * oxr_step_record_words gives the record's size in int64 words.
+ */
+size_t oxr_step_record_words(int32_t capacity, int32_t tokens_per_seq, int32_t width);
+int oxr_unpack_step_inputs(const int64_t* record, int32_t capacity, int32_t bucket, int32_t tokens_per_seq,
+                           int32_t width, int32_t scratch_block, int32_t block_size, int64_t* ids,
+                           int64_t* positions, int64_t* slots, int32_t* seq_lens, int32_t* table,
+                           oxr_stream_t stream);
 
 /*
  * (4c) Longest-prefix greedy acceptance + length rollback.
@@ -101,14 +126,14 @@ int oxr_accept(const int32_t* draft, const int32_t* draft_len, int32_t k, const 
 
 /*
  * (2) Fused q/k RMSNorm + NeoX RoPE + paged KV-cache write.
- * Replaces kernels.qk_norm_rope_store / _launch (oxr_runtime/kernels.py:150-178):
+ * Replaces kernels.qk_norm_rope_store / _launch (oxr_runtime/kernels.py:102-130):
  * qkv bf16 [n, (H + 2*KV) * 128]; q_weight, k_weight bf16 [128]; cos, sin bf16
  * [n, 64]; slots int64 [n]; k_cache, v_cache bf16 [num_slots, KV, 128] (the
  * reference's [blocks, block_size, KV, 128] viewed flat).  Writes q_out bf16
  * [n, H, 128] and, when k_out / v_out are non-null (need_kv=True), contiguous
  * k_out / v_out bf16 [n, KV, 128].  num_slots = blocks * block_size; a slot
  * outside [0, num_slots) is skipped instead of written out of bounds.  Rounding chain and the sum-of-squares
- * addition tree follow kernels.py:79-111 and 181-213; rsqrt is 1/sqrt with
+ * addition tree follow kernels.py:31-63 and 133-165; rsqrt is 1/sqrt with
  * both operations correctly rounded.  head_dim must be 128.
  */
 int oxr_qk_norm_rope_store(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
@@ -264,6 +289,21 @@ size_t oxr_lm_head_workspace_bytes(int64_t m, int64_t vocab);
 int oxr_lm_head_argmax(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
                        oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes,
                        oxr_stream_t stream);
+
+/*
+ * (4d) Argmax of logits the caller holds: logits.argmax(dim=-1) of the eager
+ * verify path (engine.py:726) and of the acceptance workload's fp32 logits.
+ * logits [rows, ld] of dtype OXR_DTYPE_F32 or OXR_DTYPE_BF16 (the first
+ * `vocab` columns of each row are compared); predicted int64 [rows] = the
+ * first index of the largest value (NaN counts as largest, -0 == +0), as
+ * torch.argmax.  workspace: oxr_argmax_workspace_bytes(rows, vocab) bytes
+ * (per-chunk maxima; no initial contents needed).  rows <= 65535.
+ */
+#define OXR_DTYPE_F32 0
+#define OXR_DTYPE_BF16 1
+size_t oxr_argmax_workspace_bytes(int64_t rows, int64_t vocab);
+int oxr_argmax(const void* logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t ld, int64_t* predicted,
+               void* workspace, size_t workspace_bytes, oxr_stream_t stream);
 
 /*
  * (3c) Variable-length (prefill) attention.  Replaces attention.varlen

@@ -12,7 +12,7 @@ Modules and the reference code each follows:
 - ``bf16``       bfloat16 round-to-nearest-even helpers (torch CPU convention).
 - ``ngram``      speculative.py:12-48 (``NgramProposer``, ``accept``), as the
                  reference's dict and as the closed form "largest (m(p), p)".
-- ``norm_rope``  kernels.py:181-213 (``qk_norm_rope_store_reference``,
+- ``norm_rope``  kernels.py:133-165 (``qk_norm_rope_store_reference``,
                  ``_sum_squares_reference``).
 - ``attention``  attention.py:96-109 with the math of the reference test stub
                  (tests/test_language_fused.py:19-57).

@@ -3,15 +3,23 @@
 Restates ``LanguageModel.extend`` / ``logits`` and the step around them
 (oxr_runtime/language.py:69-104, 201-214, 247-269, 301-317; decode_graph.py:161-167),
 with attention as the reference test stub (tests/test_language_fused.py:19-57) and the
-fused q/k norm + RoPE + KV write as ``qk_norm_rope_store_reference`` (kernels.py:181-203,
+fused q/k norm + RoPE + KV write as ``qk_norm_rope_store_reference`` (kernels.py:133-155,
 through ``oracle.norm_rope``).  Rounding points are the reference's: bf16 activations,
 bf16 ``nn.Linear`` outputs (fp32 accumulation), fp32 norms, residual stored in bf16 before
 it is normalised, fp32 softmax.
+
+Pinned (tests/test_oracle_decoder.py) by golden vectors the reference's own
+``LanguageModel.extend`` wrote (tests/golden/make_golden_decoder.py): hidden states, cache rows,
+logits and argmax bit for bit, at GQA 4/2 with S=4 and GQA 16/8 with S=9; by the same forward
+computed from the equations without rounding; and by the reference's extend == full-sequence
+invariant.
 
 It is also the CPU baseline ``bench.py`` times (torch on the host's cores).
 """
 
 from __future__ import annotations
+
+from typing import NamedTuple
 
 import numpy as np
 import torch
@@ -61,8 +69,8 @@ def paged_extend(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
 
 
 def qk_norm_rope_store(qkv, q_weight, k_weight, cos, sin, eps, k_cache, v_cache, slots, H, KV, D):
-    """kernels.py:181-203: q/k through ``oracle.norm_rope.norm_rope`` (bit-identical to the
-    reference function), then the cache rows at ``slots`` are written (kernels.py:200-202)."""
+    """kernels.py:133-155: q/k through ``oracle.norm_rope.norm_rope`` (bit-identical to the
+    reference function), then the cache rows at ``slots`` are written (kernels.py:152-154)."""
     n = qkv.shape[0]
     heads = _bits(qkv).reshape(n, H + 2 * KV, D)
     c, s_ = _bits(cos), _bits(sin)
@@ -116,12 +124,32 @@ def logits(weights, hidden: torch.Tensor) -> torch.Tensor:
     return F.linear(hidden, weights.lm_head)
 
 
-def verify_step(config, weights, histories, seq_lens, block_table, k, max_n, cache_k, cache_v, block_size):
-    """One speculative step as Engine._speculate performs it (engine.py:674-737) with graph width
-    S = k + 1: draft per sequence, assemble rows, extend, greedy ids, accept.  Returns
-    (drafts, predicted [B, S], taken per sequence, new seq_lens)."""
-    s = k + 1
-    drafts = [ngram.NgramIndex(h, max_n).propose(list(h), k) for h in histories]
+class VerifyStep(NamedTuple):
+    drafts: list[list[int]]  # per sequence, as propose() returns them
+    predicted: torch.Tensor  # int64 [B, S]: the oracle's greedy ids
+    taken: list[list[int]]   # per sequence: accept(draft, predicted row)
+    new_lens: list[int]      # seq.length after the step
+    logits: torch.Tensor     # bf16 [B * S, vocab]
+
+
+def drafts_for(histories, seq_lens, k, max_n, *, max_tokens=None, max_positions=None) -> list[list[int]]:
+    """engine.py:675-684: each sequence's draft from the ids it generated, at most
+    ``min(k, max(room, 0))`` long with room = min(max_tokens - len(output) - 1,
+    max_positions - length - 1) (a limit left out is no limit)."""
+    out = []
+    for b, h in enumerate(histories):
+        room = k
+        if max_tokens is not None:
+            room = min(room, int(max_tokens[b]) - len(h) - 1)
+        if max_positions is not None:
+            room = min(room, int(max_positions) - int(seq_lens[b]) - 1)
+        out.append(ngram.NgramIndex(h, max_n).propose(list(h), min(k, max(room, 0))))
+    return out
+
+
+def verify_rows(histories, drafts, seq_lens, block_table, s, block_size):
+    """engine.py:700-710: row b is [output[-1], *draft, 0 ...] of width S at positions length + j,
+    slots through the block table (language.py:320-322); seq_lens length + S."""
     ids, positions, slots = [], [], []
     for b, (h, draft) in enumerate(zip(histories, drafts)):
         row = [h[-1], *draft] + [0] * (s - 1 - len(draft))
@@ -131,9 +159,26 @@ def verify_step(config, weights, histories, seq_lens, block_table, k, max_n, cac
             positions.append(pos)
             slots.append(int(block_table[b, pos // block_size]) * block_size + pos % block_size)
     attn_lens = torch.tensor([int(x) + s for x in seq_lens], dtype=torch.int32)
-    hidden = extend(config, weights, torch.tensor(ids), torch.tensor(positions), torch.tensor(slots), attn_lens,
-                    torch.from_numpy(np.asarray(block_table)), s, cache_k, cache_v)
-    predicted = logits(weights, hidden).argmax(-1).view(len(histories), s)
-    taken = [ngram.accept(d, predicted[b, : len(d) + 1].tolist()) for b, d in enumerate(drafts)]
-    new_lens = [int(seq_lens[b]) + len(t) for b, t in enumerate(taken)]
-    return drafts, predicted, taken, new_lens
+    return torch.tensor(ids), torch.tensor(positions), torch.tensor(slots), attn_lens
+
+
+def accept_step(drafts, predicted, seq_lens) -> tuple[list[list[int]], list[int]]:
+    """engine.py:729-734: taken = accept(draft, row[:len(draft) + 1]); length += len(taken)."""
+    rows = predicted.tolist() if isinstance(predicted, torch.Tensor) else [list(r) for r in predicted]
+    taken = [ngram.accept(d, rows[b][: len(d) + 1]) for b, d in enumerate(drafts)]
+    return taken, [int(seq_lens[b]) + len(t) for b, t in enumerate(taken)]
+
+
+def verify_step(config, weights, histories, seq_lens, block_table, k, max_n, cache_k, cache_v, block_size, *,
+                max_tokens=None, max_positions=None) -> VerifyStep:
+    """One speculative step as Engine._speculate performs it (engine.py:674-737) with graph width
+    S = k + 1: draft per sequence, assemble rows, extend, greedy ids, accept."""
+    s = k + 1
+    drafts = drafts_for(histories, seq_lens, k, max_n, max_tokens=max_tokens, max_positions=max_positions)
+    ids, positions, slots, attn_lens = verify_rows(histories, drafts, seq_lens, block_table, s, block_size)
+    hidden = extend(config, weights, ids, positions, slots, attn_lens, torch.from_numpy(np.asarray(block_table)), s,
+                    cache_k, cache_v)
+    out = logits(weights, hidden)
+    predicted = out.argmax(-1).view(len(histories), s)
+    taken, new_lens = accept_step(drafts, predicted, seq_lens)
+    return VerifyStep(drafts, predicted, taken, new_lens, out)

@@ -1,16 +1,16 @@
 """Fused q/k RMSNorm + NeoX RoPE + paged KV write on the CPU (test infrastructure only).
 
 Restates ``qk_norm_rope_store_reference`` and ``_sum_squares_reference``
-(oxr_runtime/kernels.py:181-213) in numpy float32 with explicit bf16 rounding:
+(oxr_runtime/kernels.py:133-165) in numpy float32 with explicit bf16 rounding:
 
     h   = f32(x)
-    var = (S(h[:64]) + S(h[64:])) / 128        S: kernels.py:206-213 tree
+    var = (S(h[:64]) + S(h[64:])) / 128        S: kernels.py:158-165 tree
     h   = h * rsqrt(var + eps)                  rsqrt = 1 / sqrt, both fp32 IEEE
-    y   = f32(bf16(w * bf16(h)))                kernels.py:194
-    out = bf16(cat(y1*c - y2*s, y1*s + y2*c))   kernels.py:195-197, c, s = f32(bf16 table)
+    y   = f32(bf16(w * bf16(h)))                kernels.py:146
+    out = bf16(cat(y1*c - y2*s, y1*s + y2*c))   kernels.py:147-149, c, s = f32(bf16 table)
 
 then ``k_cache.view(-1, KV, D)[slots] = k`` and ``v_cache...[slots] = v``
-(kernels.py:200-202).  torch's CPU ``rsqrt`` equals float32 ``1 / sqrt`` bit for
+(kernels.py:152-154).  torch's CPU ``rsqrt`` equals float32 ``1 / sqrt`` bit for
 bit (tests/test_oracle_norm_rope.py checks it), and the whole chain is pinned
 against vectors written by the reference function itself
 (tests/golden/make_golden.py).
@@ -24,7 +24,7 @@ from . import bf16
 
 
 def sum_squares(x: np.ndarray) -> np.ndarray:
-    """Sum of squares over the last axis (64 values) in the order of kernels.py:206-213:
+    """Sum of squares over the last axis (64 values) in the order of kernels.py:158-165:
     split into two chunks of 32, pairwise adds at strides 16, 8, 4, 2, 1 inside each,
     then chunk 0 + chunk 1."""
     assert x.shape[-1] == 64
@@ -58,7 +58,7 @@ def qk_norm_rope_store(
     sin_bits: np.ndarray, eps: float, k_cache_bits: np.ndarray, v_cache_bits: np.ndarray, slots: np.ndarray,
     num_heads: int, num_kv_heads: int, head_dim: int, *, need_kv: bool,
 ):
-    """kernels.py:181-203.  Caches are uint16 arrays whose flat view is [slots, KV, D]; they are
+    """kernels.py:133-155.  Caches are uint16 arrays whose flat view is [slots, KV, D]; they are
     written in place.  Returns (q, k | None, v | None) as uint16 arrays."""
     n = qkv_bits.shape[0]
     heads = qkv_bits.reshape(n, num_heads + 2 * num_kv_heads, head_dim)

@@ -29,8 +29,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_ngram_propose": (ctypes.c_int, [_P, _I64, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P]),
     "oxr_propose_verify_inputs": (
         ctypes.c_int,
-        [_P, _I64, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
+        [_P, _I64, _P, _I32, _I32, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P, _P, _P],
     ),
+    "oxr_step_record_words": (ctypes.c_size_t, [_I32, _I32, _I32]),
+    "oxr_unpack_step_inputs": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
     "oxr_accept": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P]),
     "oxr_paged_extend_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _I32]),
     "oxr_paged_extend": (
@@ -54,6 +56,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_gemm_bf16_partial": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P]),
     "oxr_lm_head_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "oxr_lm_head_argmax": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "oxr_argmax_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "oxr_argmax": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "oxr_varlen_attention": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P]),
     "oxr_packed_weight_elems": (ctypes.c_size_t, [_I64, _I64]),
     "oxr_pack_weight_bf16": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),

@@ -325,6 +325,69 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint64_t* __re
 }
 
 
+// Argmax of logits the caller already holds (fp32 or bf16 [rows, ld], first `vocab` columns):
+// the eager path's logits.argmax(dim=-1) (engine.py:726).  Each row is cut into `gridDim.x`
+// column chunks, one workgroup each, so a few rows still spread over the chip; every thread
+// keeps the best key of its strided 16-byte pieces, the workgroup reduces them, and
+// argmax_reduce_kernel merges the chunks (the keys order values, then lower columns first).
+template <typename T>
+__device__ __forceinline__ uint32_t logit_bits(T v);
+template <>
+__device__ __forceinline__ uint32_t logit_bits<float>(float v) { return __float_as_uint(v); }
+template <>
+__device__ __forceinline__ uint32_t logit_bits<bf16_t>(bf16_t v) { return (uint32_t)v << 16; }
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ logits, int64_t ld, int64_t vocab,
+                                                          int rows, uint64_t* __restrict__ best) {
+  constexpr int kPer = 16 / sizeof(T);  // elements per 16-byte piece
+  __shared__ uint64_t part[256 / kWave];
+  const int row = blockIdx.y;
+  const T* src = logits + (int64_t)row * ld;
+  const int64_t pieces = (vocab + kPer - 1) / kPer;
+  const int64_t per_chunk = (pieces + gridDim.x - 1) / gridDim.x;
+  const int64_t p0 = (int64_t)blockIdx.x * per_chunk;
+  const int64_t p1 = p0 + per_chunk < pieces ? p0 + per_chunk : pieces;
+  uint64_t b = 0;
+  for (int64_t p = p0 + threadIdx.x; p < p1; p += blockDim.x) {
+    const int64_t c0 = p * kPer;
+    T v[kPer];
+    if (kVec && c0 + kPer <= vocab) {
+      *reinterpret_cast<u32x4*>(v) = ld128(src + c0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) v[e] = c0 + e < vocab ? src[c0 + e] : src[0];
+    }
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      if (c0 + e < vocab) {
+        const uint64_t key = argmax_key(logit_bits<T>(v[e]), (uint32_t)(c0 + e));
+        b = key > b ? key : b;
+      }
+    }
+  }
+#pragma unroll
+  for (int mask = 1; mask < kWave; mask <<= 1) {
+    const uint64_t o = shfl_xor_u64(b, mask);
+    b = o > b ? o : b;
+  }
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 256 / kWave; ++w) b = part[w] > b ? part[w] : b;
+    b = part[0] > b ? part[0] : b;
+    best[(int64_t)blockIdx.x * rows + row] = b;
+  }
+}
+
+// Column chunks per row: about 1024 workgroups in all, each at least 4096 columns.
+int argmax_chunks(int64_t rows, int64_t vocab) {
+  int64_t c = (1024 + rows - 1) / rows;
+  const int64_t by_cols = (vocab + 4095) / 4096;
+  c = c < by_cols ? c : by_cols;
+  return (int)(c < 1 ? 1 : (c > 1024 ? 1024 : c));
+}
+
 // ---------------------------------------------------------------------------
 // Persistent LM head for M <= 32 token rows.  Every weight byte is read once,
 // so the kernel is bound by the rate at which the CUs' vector memory path
@@ -1015,4 +1078,40 @@ extern "C" int oxr_lm_head_argmax_packed(const oxr_bf16* hidden, int64_t m, cons
                                          void* workspace, size_t workspace_bytes, oxr_stream_t stream) {
   return oxr::lm_head_entry(hidden, m, weight_packed, hidden_size, vocab, logits, predicted, workspace,
                             workspace_bytes, true, stream);
+}
+
+extern "C" size_t oxr_argmax_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  return (size_t)oxr::argmax_chunks(rows, vocab) * (size_t)rows * sizeof(uint64_t);
+}
+
+extern "C" int oxr_argmax(const void* logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t ld,
+                          int64_t* predicted, void* workspace, size_t workspace_bytes, oxr_stream_t stream) {
+  using namespace oxr;
+  OXR_RETURN_IF(rows < 0 || vocab <= 0 || ld < vocab, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(dtype != OXR_DTYPE_F32 && dtype != OXR_DTYPE_BF16, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(rows > 65535 || vocab > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
+  if (rows == 0) return OXR_OK;
+  OXR_RETURN_IF(!logits || !predicted, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(!workspace || workspace_bytes < oxr_argmax_workspace_bytes(rows, vocab), OXR_ERR_WORKSPACE);
+  hipStream_t s = (hipStream_t)stream;
+  const int chunks = argmax_chunks(rows, vocab);
+  uint64_t* best = static_cast<uint64_t*>(workspace);
+  const dim3 grid((unsigned)chunks, (unsigned)rows), block(256);
+  const size_t elem = dtype == OXR_DTYPE_F32 ? 4 : 2;
+  const bool vec = ((uintptr_t)logits % 16 == 0) && ((size_t)ld * elem) % 16 == 0;
+  if (dtype == OXR_DTYPE_F32) {
+    const float* p = static_cast<const float*>(logits);
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<float, true>), grid, block, 0, s, p, ld, vocab, (int)rows, best);
+    else hipLaunchKernelGGL((argmax_rows_kernel<float, false>), grid, block, 0, s, p, ld, vocab, (int)rows, best);
+  } else {
+    const bf16_t* p = static_cast<const bf16_t*>(logits);
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<bf16_t, true>), grid, block, 0, s, p, ld, vocab, (int)rows, best);
+    else hipLaunchKernelGGL((argmax_rows_kernel<bf16_t, false>), grid, block, 0, s, p, ld, vocab, (int)rows, best);
+  }
+  int st = OXR_LAUNCH_STATUS();
+  if (st) return st;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)rows), dim3(256), 0, s, static_cast<const uint64_t*>(best),
+                     chunks, (int)rows, predicted);
+  return OXR_LAUNCH_STATUS();
 }

@@ -35,6 +35,8 @@ struct VerifyInputs {
   int64_t* positions;  // [B * S]
   int64_t* slots;      // [B * S]
   int32_t* attn_seq_lens;  // [B] seq_len + S
+  const int32_t* max_tokens;  // optional [B]: generated-token limit of each sequence
+  int max_positions;          // > 0: the position table's size
 };
 
 template <bool kAssemble>
@@ -121,6 +123,12 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
 
   int kb = k;
   if (k_limit) kb = max(0, min(k, k_limit[b]));
+  if constexpr (kAssemble) {
+    // Room left for drafts (engine.py:683-684): the accepted drafts plus the model's own token
+    // must stay within max_tokens, and the step's positions within max_positions.
+    if (vi.max_tokens) kb = max(0, min(kb, vi.max_tokens[b] - L - 1));
+    if (vi.max_positions > 0) kb = max(0, min(kb, vi.max_positions - vi.seq_len[b] - 1));
+  }
   int len = 0;
   if (best_n > 0) len = min(kb, L - best_p);
   for (int j = tid; j < k; j += kThreads) draft[(int64_t)b * k + j] = (j < len) ? h[best_p + j] : 0;
@@ -130,7 +138,8 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
     // Row b of the verify batch: [pending token, *draft, 0-padding], each at
     // position seq_len + j and slot slot_of(blocks, seq_len + j)
     // (engine.py:700-710, language.py:320-322).  A position past the block
-    // table gets slot -1, which the KV write skips.
+    // table, or on a negative (unallocated) table entry, gets slot -1, which
+    // the KV write skips.
     const int S = vi.tokens_per_seq;
     const int base_len = vi.seq_len[b];
     for (int j = tid; j < S; j += kThreads) {
@@ -140,8 +149,10 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
       const int64_t pos = (int64_t)base_len + j;
       const int64_t blk = pos / vi.block_size;
       int64_t slot = -1;
-      if (pos >= 0 && blk < vi.table_stride)
-        slot = (int64_t)vi.block_table[(int64_t)b * vi.table_stride + blk] * vi.block_size + pos % vi.block_size;
+      if (pos >= 0 && blk < vi.table_stride) {
+        const int32_t page = vi.block_table[(int64_t)b * vi.table_stride + blk];
+        if (page >= 0) slot = (int64_t)page * vi.block_size + pos % vi.block_size;
+      }
       const int64_t row = (int64_t)b * S + j;
       vi.ids[row] = id;
       vi.positions[row] = pos;
@@ -171,8 +182,9 @@ extern "C" int oxr_propose_verify_inputs(const int32_t* history, int64_t history
                                          const int32_t* history_len, int32_t batch, int32_t max_n, int32_t k,
                                          const int32_t* k_limit, const int32_t* seq_len, const int32_t* block_table,
                                          int64_t table_stride, int32_t block_size, int32_t tokens_per_seq,
-                                         int32_t* draft, int32_t* draft_len, int64_t* ids, int64_t* positions,
-                                         int64_t* slots, int32_t* attn_seq_lens, oxr_stream_t stream) {
+                                         const int32_t* max_tokens, int32_t max_positions, int32_t* draft,
+                                         int32_t* draft_len, int64_t* ids, int64_t* positions, int64_t* slots,
+                                         int32_t* attn_seq_lens, oxr_stream_t stream) {
   using namespace oxr;
   OXR_RETURN_IF(batch < 0 || k < 0 || history_stride < 0 || table_stride < 0 || block_size <= 0,
                 OXR_ERR_INVALID_ARG);
@@ -183,7 +195,7 @@ extern "C" int oxr_propose_verify_inputs(const int32_t* history, int64_t history
                     !positions || !slots || !attn_seq_lens,
                 OXR_ERR_INVALID_ARG);
   VerifyInputs vi{seq_len, block_table, table_stride, block_size, tokens_per_seq, ids, positions, slots,
-                  attn_seq_lens};
+                  attn_seq_lens, max_tokens, max_positions};
   hipLaunchKernelGGL(ngram_propose_kernel<true>, dim3(batch), dim3(kThreads), 0, (hipStream_t)stream, history,
                      history_stride, history_len, nullptr, max_n, k, k_limit, draft, draft_len, vi);
   return OXR_LAUNCH_STATUS();

@@ -4,10 +4,10 @@
 //
 // One head (128 bf16 = 256 B) is owned by 16 consecutive lanes (s = lane % 16),
 // each holding 8 consecutive elements.  Bit-exact with the reference rounding
-// chain (oxr_runtime/kernels.py:95-111):
+// chain (oxr_runtime/kernels.py:47-63):
 //   h   = f32(x)
 //   var = (S(h[0:64]) + S(h[64:128])) / 128, S = the fixed addition tree of
-//         kernels.py:79-92 / 206-213: per 32-element chunk pairwise adds at
+//         kernels.py:31-44 / 158-165: per 32-element chunk pairwise adds at
 //         element strides 16, 8, 4, 2, 1, then chunk0 + chunk1
 //   r   = 1 / sqrt(var + eps)            (both correctly rounded)
 //   y   = f32(bf16(w * bf16(h * r)))     (w * bf16 is exact in fp32)

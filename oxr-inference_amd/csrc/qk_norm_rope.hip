@@ -1,7 +1,7 @@
 // Fused q/k RMSNorm + NeoX RoPE + paged KV-cache write (gfx950).
 //
-// Replaces the Triton kernel of oxr_runtime/kernels.py:114-147 and its CPU
-// restatement kernels.py:181-213.  One head (128 bf16 = 256 B) is owned by 16
+// Replaces the Triton kernel of oxr_runtime/kernels.py:66-99 and its CPU
+// restatement kernels.py:133-165.  One head (128 bf16 = 256 B) is owned by 16
 // lanes, each holding 8 consecutive elements loaded with one 128-bit load, so
 // a 64-lane wave works on 4 heads and every load and store is a full 128-bit
 // access.  The work is flattened over (token, head) so the grid scales with

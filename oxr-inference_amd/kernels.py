@@ -1,8 +1,8 @@
 """Fused q/k RMSNorm + RoPE + paged KV write: the drop-in for oxr_runtime/kernels.py.
 
-``qk_norm_rope_store`` keeps the reference signature (kernels.py:150-161) and runs the
+``qk_norm_rope_store`` keeps the reference signature (kernels.py:102-113) and runs the
 hand-written gfx950 kernel ``oxr_qk_norm_rope_store`` (csrc/qk_norm_rope.hip).  The
-reference dispatches CPU tensors to a torch restatement (kernels.py:159-160); this build
+reference dispatches CPU tensors to a torch restatement (kernels.py:111-112); this build
 has no CPU path and raises for CPU tensors instead.
 """
 

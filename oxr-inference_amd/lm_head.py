@@ -58,3 +58,26 @@ def lm_head_argmax(
 def logits(hidden: torch.Tensor, weight: Weight) -> torch.Tensor:
     """``LanguageModel.logits``: bf16 ``hidden @ weight.T`` (language.py:213-214)."""
     return lm_head_argmax(hidden, weight, return_logits=True)[1]
+
+
+def argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None,
+           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``logits.argmax(dim=-1)`` (engine.py:726) for fp32 or bf16 logits ``[..., vocab]`` already in
+    memory: int64 ``[...]``, the first index of each row's largest value (NaN counts as largest)."""
+    device = _lib.require_gpu(logits, name="argmax")
+    _lib.require(logits.dtype in (torch.float32, torch.bfloat16), "argmax: fp32 or bf16 logits")
+    _lib.require(logits.dim() >= 1 and logits.shape[-1] > 0 and logits.stride(-1) == 1, "argmax: contiguous rows")
+    vocab = logits.shape[-1]
+    rows2d = logits.reshape(-1, vocab)
+    _lib.require(rows2d.dim() == 2 and rows2d.stride(-1) == 1, "argmax: rows must be evenly strided")
+    rows = rows2d.shape[0]
+    if out is None:
+        out = torch.empty(logits.shape[:-1], dtype=torch.int64, device=device)
+    _lib.require(out.dtype == torch.int64 and out.numel() == rows and out.is_contiguous(), "argmax: out int64 [...]")
+    need = int(_lib.lib().oxr_argmax_workspace_bytes(rows, vocab))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    dtype = 0 if logits.dtype == torch.float32 else 1  # OXR_DTYPE_F32 / OXR_DTYPE_BF16
+    _lib.call("oxr_argmax", rows2d.data_ptr(), dtype, rows, vocab, rows2d.stride(0), out.data_ptr(),
+              workspace.data_ptr(), workspace.numel() * workspace.element_size(), _lib.stream(device))
+    return out

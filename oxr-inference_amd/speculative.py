@@ -88,11 +88,15 @@ def alloc_verify_inputs(batch: int, k: int, tokens_per_seq: int, device: torch.d
 def propose_verify_inputs(
     history: torch.Tensor, history_len: torch.Tensor, k: int, seq_len: torch.Tensor, block_table: torch.Tensor,
     block_size: int, tokens_per_seq: int, *, max_n: int = _MAX_N, k_limit: torch.Tensor | None = None,
-    out: VerifyInputs | None = None,
+    max_tokens: torch.Tensor | None = None, max_positions: int = 0, out: VerifyInputs | None = None,
 ) -> VerifyInputs:
     """Drafting plus the verify rows of engine.py:700-710, all on the GPU.  ``seq_len`` is each
-    sequence's KV length before the step (the reference's ``seq.length``)."""
-    device = _lib.require_gpu(history, history_len, seq_len, block_table, k_limit, name="propose_verify_inputs")
+    sequence's KV length before the step (the reference's ``seq.length``).  Drafts are capped by
+    the room engine.py:683-684 leaves: ``max_tokens[b] - len(history) - 1`` (when given) and
+    ``max_positions - seq_len - 1`` (when > 0).  Negative block-table entries (pages not
+    allocated) give slot -1: that row's K/V is not stored."""
+    device = _lib.require_gpu(history, history_len, seq_len, block_table, k_limit, max_tokens,
+                              name="propose_verify_inputs")
     _check_int32("history", history, 2)
     _check_int32("history_len", history_len, 1)
     _check_int32("seq_len", seq_len, 1)
@@ -100,13 +104,17 @@ def propose_verify_inputs(
     b = history.shape[0]
     _lib.require(tokens_per_seq >= k + 1, "tokens_per_seq must be at least k + 1")
     _lib.require(block_table.shape[0] >= b and history_len.shape[0] == b and seq_len.shape[0] == b, "batch sizes differ")
+    if max_tokens is not None:
+        _check_int32("max_tokens", max_tokens, 1)
+        _lib.require(max_tokens.shape[0] == b, "max_tokens must be [B]")
     if out is None:
         out = alloc_verify_inputs(b, k, tokens_per_seq, device)
     _lib.call(
         "oxr_propose_verify_inputs", history.data_ptr(), history.stride(0), history_len.data_ptr(), b, max_n, k,
         _lib.ptr(k_limit), seq_len.data_ptr(), block_table.data_ptr(), block_table.stride(0), block_size,
-        tokens_per_seq, out.draft.data_ptr(), out.draft_len.data_ptr(), out.ids.data_ptr(), out.positions.data_ptr(),
-        out.slots.data_ptr(), out.attn_seq_lens.data_ptr(), _lib.stream(device),
+        tokens_per_seq, _lib.ptr(max_tokens), int(max_positions), out.draft.data_ptr(), out.draft_len.data_ptr(),
+        out.ids.data_ptr(), out.positions.data_ptr(), out.slots.data_ptr(), out.attn_seq_lens.data_ptr(),
+        _lib.stream(device),
     )
     return out
 

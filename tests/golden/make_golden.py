@@ -1,7 +1,7 @@
 """Write golden vectors for the fused q/k RMSNorm + RoPE + KV write from the reference itself.
 
-Runs ``qk_norm_rope_store_reference`` of the reference (oxr_runtime/kernels.py:181-213,
-the function its CPU path dispatches to at kernels.py:159-160) on seeded inputs and
+Runs ``qk_norm_rope_store_reference`` of the reference (oxr_runtime/kernels.py:133-165,
+the function its CPU path dispatches to at kernels.py:111-112) on seeded inputs and
 stores inputs and outputs as raw bf16 bits in ``qk_norm_rope_store.npz``.  This is the
 one function on the path whose exact bits (torch's CPU rsqrt and bf16 rounding) no
 closed form in the reference's tests pins, so its vectors come from the reference.

@@ -1,5 +1,5 @@
 """The drop-in boundary refuses CPU tensors instead of falling back to a CPU path
-(the reference dispatches CPU tensors to torch code, kernels.py:159-160; this build
+(the reference dispatches CPU tensors to torch code, kernels.py:111-112; this build
 has none), and validates shapes on the host before any launch."""
 
 from __future__ import annotations

@@ -195,3 +195,67 @@ def test_accept_batch_and_rollback() -> None:
     spec.accept_batch(d(draft), d(dlen), d(predicted), seq_len=seq_t, history=hist_t, history_len=hlen_t,
                       eos_id=eos, max_tokens=d(max_tokens), finished=fin_t)
     assert np.array_equal(seq_t.cpu().numpy()[done], before.cpu().numpy()[done])
+
+
+lm_head = pkg("lm_head")
+
+
+def _torch_argmax(a: np.ndarray) -> np.ndarray:
+    """torch.argmax on the CPU: first index of the maximum, NaN counted as the maximum."""
+    return torch.from_numpy(a).argmax(-1).numpy()
+
+
+def test_config1_planted_logits_argmax_and_accept() -> None:
+    """Workload 1's acceptance leg: drafts of the four histories (max_n 3, k 3), fp32 verify
+    logits [4, 4, 151936] ~N(0, 1) with each draft id planted as the row's strict maximum with
+    p = 0.6, argmax on the GPU, then acceptance (engine.py:726-733) -- ids, accepted lengths,
+    committed ids and the next tokens bit-exact against the oracle."""
+    hist_np = workloads.drafting_histories(seed=0)
+    rows = [h.tolist() for h in hist_np]
+    k, S = 3, 4
+    announce("config 1 drafting")
+    draft, dlen = spec.propose_batch(torch.from_numpy(hist_np).cuda(), torch.full((4,), 512, dtype=torch.int32,
+                                                                                  device="cuda"), k, max_n=3)
+    want_draft, want_len = ngram.propose_batch(rows, k, max_n=3)
+    assert np.array_equal(draft.cpu().numpy(), want_draft) and np.array_equal(dlen.cpu().numpy(), want_len)
+    logits = workloads.plant_logits(np.random.default_rng(1), want_draft, want_len, S)
+    announce("config 1 argmax + accept")
+    predicted = lm_head.argmax(torch.from_numpy(logits).cuda())
+    res = spec.accept_batch(draft, dlen, predicted)
+    want_pred = np.argmax(logits, axis=-1)
+    assert np.array_equal(predicted.cpu().numpy(), want_pred)
+    acc, com = res.accepted.cpu().numpy(), res.committed.cpu().numpy()
+    planted = 0
+    for b in range(4):
+        taken = ngram.accept(want_draft[b, : want_len[b]].tolist(), want_pred[b, : want_len[b] + 1].tolist())
+        assert acc[b] == len(taken) - 1 and com[b, : len(taken)].tolist() == taken
+        assert com[b, len(taken) - 1] == taken[-1]  # the next token: the model's own after the accepted prefix
+        planted += acc[b]
+    assert want_len.max() > 0 and planted > 0, "nothing accepted: the planted path went untested"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_edge_cases(dtype) -> None:
+    """Ties to the lowest index (also across column chunks), NaN as the maximum (first NaN),
+    -0 == +0, all -inf rows, odd widths and a row stride that breaks 16-byte alignment."""
+    rng = np.random.default_rng(3)
+    vocab = 151_936
+    a = rng.standard_normal((9, vocab)).astype(np.float32)
+    a[1, [70_000, 5, 140_000]] = 50.0            # tie across chunks -> 5
+    a[2, [9, 100_000]] = np.nan                    # first NaN
+    a[3] = -np.inf                                  # all -inf -> 0
+    a[4] = 0.0
+    a[4, :1000] = -0.0                              # -0 == +0 -> 0
+    a[5, -1] = 1e30                                 # last column
+    a[6, 151_935] = np.inf
+    a[6, 77] = np.inf                               # first +inf
+    a = torch.from_numpy(a).to(dtype)
+    announce("argmax edge cases", dtype)
+    got = lm_head.argmax(a.cuda()).cpu().numpy()
+    assert np.array_equal(got, a.float().argmax(-1).numpy()), got
+    odd = a[:, 3 : 3 + 1001].contiguous()
+    assert np.array_equal(lm_head.argmax(odd.cuda()).cpu().numpy(), odd.float().argmax(-1).numpy())
+    strided = a.cuda()[:, 1:1001]  # rows 16-byte aligned only by chance: the unvectorised form
+    assert np.array_equal(lm_head.argmax(strided).cpu().numpy(), a[:, 1:1001].float().argmax(-1).numpy())
+    batch = a[:8].reshape(2, 4, vocab)  # leading dims kept
+    assert lm_head.argmax(batch.cuda()).shape == (2, 4)

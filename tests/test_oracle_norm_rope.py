@@ -4,7 +4,7 @@
   a verify-sized case, a need_kv case and tokens chosen so that the sum-of-squares order
   changes the result; the oracle matches all of them bit for bit, and an oracle with a
   different addition order (planted here, on the CPU) fails the order case.
-- torch's CPU rsqrt (what the reference calls, kernels.py:193) equals float32 1/sqrt.
+- torch's CPU rsqrt (what the reference calls, kernels.py:145) equals float32 1/sqrt.
 - Closed-form special cases: heads of constant magnitude 2^e normalise to exactly +-1, so
   with cos=1, sin=0 the output is +-w; with cos=0, sin=1 the halves swap with the sign of
   NeoX rotation.
