@@ -29,6 +29,7 @@ extern "C" {
 #define OXR_ERR_INVALID_ARG (-1)   /* null pointer, negative or inconsistent size */
 #define OXR_ERR_UNSUPPORTED (-2)   /* shape outside what the kernels implement     */
 #define OXR_ERR_WORKSPACE (-3)     /* workspace missing or smaller than required   */
+#define OXR_ERR_SCRATCH_LIMIT (-4) /* shape needs more than the static scratch holds */
 
 typedef void* oxr_stream_t; /* hipStream_t */
 typedef uint16_t oxr_bf16;  /* raw bfloat16 bits */
@@ -239,6 +240,29 @@ int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight,
                                   int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale,
                                   oxr_bf16* out, int32_t out_packed, void* workspace, size_t workspace_bytes,
                                   oxr_stream_t stream);
+
+/*
+ * (3b') (3b) without a workspace argument, allocating nothing.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops or harnesses that forbid allocation).
+ * The split partials live in a static device array of
+ * oxr_static_scratch_bytes() bytes (32 MiB) that each GPU the library runs on
+ * holds until the process ends; shapes whose oxr_paged_extend_workspace_bytes
+ * exceed it return OXR_ERR_SCRATCH_LIMIT.  The array's device address is looked
+ * up on the first call on each device, which must therefore not be inside a
+ * stream capture.  All calls on one GPU share the array: calls that overlap in
+ * time on one GPU race.  Arguments and results otherwise as (3b).
+ */
+size_t oxr_static_scratch_bytes(void);
+int oxr_qk_norm_rope_paged_extend_static(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                                         const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,
+                                         const int64_t* positions, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache,
+                                         const int64_t* slots, int64_t num_slots, const int32_t* seq_lens,
+                                         const int32_t* block_table, int64_t table_stride, int32_t batch,
+                                         int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                         int32_t max_seq_len, float scale, oxr_bf16* out, int32_t out_packed,
+                                         oxr_stream_t stream);
 
 /*
  * (4a) Weight-streaming bf16 GEMM Y = X * W^T with a fused epilogue.

@@ -40,6 +40,7 @@
 //     per-row rescale is a per-lane scalar.
 // The next 32 keys' K and V are loaded before the current ones are used.
 #include <algorithm>
+#include <mutex>
 
 #include "norm_rope.h"
 
@@ -642,4 +643,67 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
   return launch_paged_extend(nullptr, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
                              num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
                              out_packed ? 1 : 0, workspace, workspace_bytes, &ra, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// The same launch with no workspace argument, for callers that cannot allocate
+// (code under HIP graph capture, serving loops that forbid allocation): the
+// split partials live in `scratch`, a static device array each GPU holds until
+// the process ends.  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in); the device address comes from
+// hipGetSymbolAddress once per device, on the entry point's first call there.
+// The partials need no initial contents, so nothing is cleared.  Calls on one
+// GPU share the array: calls that overlap in time on one GPU race.
+// ---------------------------------------------------------------------------
+namespace oxr {
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+constexpr int kScratchMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex scratch_mutex;
+void* scratch_ptr[kScratchMaxDevices] = {};
+
+// The current device's address of `scratch` (set up on first use), or an error status.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kScratchMaxDevices) return OXR_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return OXR_ERR_INVALID_ARG;
+    scratch_ptr[dev] = ptr;
+  }
+  *out = scratch_ptr[dev];
+  return OXR_OK;
+}
+
+}  // namespace
+}  // namespace oxr
+
+extern "C" size_t oxr_static_scratch_bytes(void) { return oxr::kScratchBytes; }
+
+extern "C" int oxr_qk_norm_rope_paged_extend_static(
+    const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight, const oxr_bf16* cos_table,
+    const oxr_bf16* sin_table, int64_t table_rows, const int64_t* positions, float eps, oxr_bf16* k_cache,
+    oxr_bf16* v_cache, const int64_t* slots, int64_t num_slots, const int32_t* seq_lens, const int32_t* block_table,
+    int64_t table_stride, int32_t batch, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
+    int32_t out_packed, oxr_stream_t stream) {
+  using namespace oxr;
+  if (batch > 0 && num_kv_heads > 0 && max_seq_len > 0 &&
+      oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len) > kScratchBytes)
+    return OXR_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  const int st = scratch_address(&ws);
+  if (st) return st;
+  return oxr_qk_norm_rope_paged_extend(qkv, q_weight, k_weight, cos_table, sin_table, table_rows, positions, eps,
+                                       k_cache, v_cache, slots, num_slots, seq_lens, block_table, table_stride, batch,
+                                       tokens_per_seq, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                                       max_seq_len, scale, out, out_packed, ws, kScratchBytes, stream);
 }

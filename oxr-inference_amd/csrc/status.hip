@@ -13,6 +13,9 @@ extern "C" const char* oxr_status_string(int status) {
       return "unsupported shape for the gfx950 kernels";
     case OXR_ERR_WORKSPACE:
       return "workspace missing or smaller than required";
+    case OXR_ERR_SCRATCH_LIMIT:
+      return "the shape needs more scratch than the library's static scratch array holds "
+             "(see oxr_static_scratch_bytes); use the entry point that takes a workspace";
     default:
       break;
   }
