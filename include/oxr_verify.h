@@ -198,7 +198,7 @@ int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t r
  * in the cache); block_table int32 [B, table_stride].  Token s of sequence b
  * attends keys [0, seq_lens[b] - S + s] of kv head h / (H / KV) with scores
  * q.k * scale and an fp32 softmax; out bf16 [B, S, H, 128].
- * Requires H % KV == 0, S * (H / KV) <= 16, block_size a power of two >= 16,
+ * Requires H % KV == 0, S * (H / KV) <= 32, block_size a power of two >= 16,
  * max_seq_len <= table_stride * block_size; contexts longer than max_seq_len
  * are clamped to it.  workspace: at least
  * oxr_paged_extend_workspace_bytes(batch, KV, max_seq_len) bytes of device
@@ -228,7 +228,7 @@ int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16*
  * assembles them).  A slot outside [0, num_slots) is not stored, as in
  * (2b), but the token's computed K/V still take part in the attention.
  * Same requirements and workspace as (3), and also
- * tokens_per_seq <= 8 with tokens_per_seq * (H / KV + 2) <= 32; bit-identical
+ * tokens_per_seq <= 16 with tokens_per_seq * (H / KV + 2) <= 64; bit-identical
  * q, cache rows and output to (2b) then (3).
  */
 int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
@@ -246,9 +246,11 @@ int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight,
  * in the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops or harnesses that forbid allocation).
  * The split partials live in a static device array of
- * oxr_static_scratch_bytes() bytes (32 MiB) that each GPU the library runs on
- * holds until the process ends; shapes whose oxr_paged_extend_workspace_bytes
- * exceed it return OXR_ERR_SCRATCH_LIMIT.  The array's device address is looked
+ * oxr_static_scratch_bytes() bytes (16.25 MiB) that each GPU the library runs
+ * on holds until the process ends.  Every shape (3b) accepts fits it (a launch
+ * splits contexts into at most 1020 partial units); a shape whose
+ * oxr_paged_extend_workspace_bytes exceeded it would return
+ * OXR_ERR_SCRATCH_LIMIT.  The array's device address is looked
  * up on the first call on each device, which must therefore not be inside a
  * stream capture.  All calls on one GPU share the array: calls that overlap in
  * time on one GPU race.  Arguments and results otherwise as (3b).
@@ -276,7 +278,8 @@ int oxr_qk_norm_rope_paged_extend_static(const oxr_bf16* qkv, const oxr_bf16* q_
  *   OXR_EPI_ADD_RESIDUAL y = bf16(bf16(x @ w^T) + y), in place: the residual
  *                        add of _add_rms_norm (language.py:94-99)
  * x bf16 [m, ldx] (first k columns used), w bf16 [rows, k] row-major, fp32
- * accumulation.  m <= 64, k a multiple of 128, x and w 16-byte aligned.
+ * accumulation.  m <= 256 (one launch per 64 rows over the same weight), k a
+ * multiple of 128, x and w 16-byte aligned.
  */
 #define OXR_EPI_STORE 0
 #define OXR_EPI_SILU_MUL 1

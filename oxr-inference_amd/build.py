@@ -14,6 +14,12 @@ Flags that matter for results:
   instructions (``v_pk_*_f32``), which have given intermittently wrong results
   on this machine pool.
 
+Every kernel must run without scratch memory: the build reads the compiler's
+resource-usage remarks and fails if any kernel has a nonzero ``ScratchSize``.
+Several kernels wait on hand-counted vector-memory counts (``s_waitcnt vmcnt``)
+that hold only while no compiler-inserted scratch traffic shares the counter,
+and a spill would also cost the register budget the designs are sized for.
+
 Usage: ``python oxr-inference_amd/build.py`` (or ``__graft_entry__.build()``).
 """
 
@@ -21,6 +27,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -55,12 +62,32 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
 
 
+_NAME = re.compile(r"remark: Function Name: (\S+)")
+_SCRATCH = re.compile(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)")
+
+
+def scratch_users(remarks: str) -> list[tuple[str, int]]:
+    """(kernel, bytes per lane) for every kernel whose resource-usage remark reports scratch."""
+    users, name = [], None
+    for line in remarks.splitlines():
+        if m := _NAME.search(line):
+            name = m.group(1)
+        elif (m := _SCRATCH.search(line)) and name is not None and int(m.group(1)) > 0:
+            users.append((name, int(m.group(1))))
+    return users
+
+
 def _compile(source: Path) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(source), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{' '.join(cmd)}\n{proc.stdout}{proc.stderr}")
+    users = scratch_users(proc.stderr)
+    if users:
+        obj.unlink(missing_ok=True)
+        listing = "\n".join(f"  {name}: {size} bytes/lane" for name, size in users)
+        raise RuntimeError(f"{source.name}: kernels use scratch memory (register spills), not allowed:\n{listing}")
     return obj
 
 

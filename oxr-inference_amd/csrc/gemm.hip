@@ -82,7 +82,8 @@ struct GemmArgs {
   int64_t ldy;
   int y_packed;     // kStore / kSiluMul: y in the packed layout with row length N (ldy unused)
   uint64_t* best;   // kArgmax: [num_tiles, M]
-  float* part;      // kPartial: [k_splits, M, N]
+  float* part;      // kPartial: [k_splits, part_rows, N], this launch's rows first
+  int64_t part_rows;
 };
 
 #ifndef OXR_NT_PART
@@ -253,7 +254,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
 #pragma unroll
       for (int a = 0; a < NA; ++a) {
         const int64_t col0 = n0 + 16 * a + 4 * g;
-        float* dst = args.part + ((int64_t)blockIdx.y * args.M + tok) * args.N + col0;
+        float* dst = args.part + ((int64_t)blockIdx.y * args.part_rows + tok) * args.N + col0;
         if (col0 + 3 < args.N) {
           if (OXR_NT_PART) __builtin_nontemporal_store(acc[a][bt], reinterpret_cast<f32x4*>(dst));
           else *reinterpret_cast<f32x4*>(dst) = acc[a][bt];
@@ -896,9 +897,15 @@ LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
   return c;
 }
 
+// Token rows one launch of gemm_kernel takes (4 tiles of 16); the entry points take up to kMaxRows
+// and run one launch per 64 rows over the same weight.  The first launch streams the weight from
+// HBM; it is at most a few tens of MB, so the later ones find it in the 256 MB Infinity Cache.
+constexpr int64_t kPassRows = 64;
+constexpr int64_t kMaxRows = 256;
+
 int check_common(const void* x, int64_t ldx, int64_t M, const void* w, int64_t K, int64_t N) {
   OXR_RETURN_IF(M < 0 || K <= 0 || N <= 0 || ldx < K, OXR_ERR_INVALID_ARG);
-  OXR_RETURN_IF(M > 64 || K % kKStep != 0, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(M > kMaxRows || K % kKStep != 0, OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(M > 0 && (!x || !w), OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(((uintptr_t)x | (uintptr_t)w) % 16 != 0 || ldx % 8 != 0, OXR_ERR_UNSUPPORTED);
   return OXR_OK;
@@ -937,13 +944,20 @@ int gemm_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int
   OXR_RETURN_IF(packed && epilogue == kSiluMul && n % 16 != 0, OXR_ERR_UNSUPPORTED);  // up rows start a tile
   OXR_RETURN_IF(yp && (epilogue == kAddResidual || n % kKStep != 0), OXR_ERR_UNSUPPORTED);
   if (m == 0) return OXR_OK;
-  GemmArgs a{x, ldx, (int)m, w, k, n, y, ldy, yp ? 1 : 0, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
   const LaunchConfig c = choose_config(n, k, false);
   const Layout layout = !packed ? kRowMajor : (xp ? kPackedWX : kPackedW);
-  if (epilogue == kSiluMul) return dispatch<kSiluMul>(a, c, layout, s);
-  if (epilogue == kAddResidual) return dispatch<kAddResidual>(a, c, layout, s);
-  return dispatch<kStore>(a, c, layout, s);
+  for (int64_t r0 = 0; r0 < m; r0 += kPassRows) {
+    // Rows [r0, r0 + 64): a packed operand's rows start r0 * row_length elements in (r0 is a
+    // multiple of 16, a whole number of tiles).
+    GemmArgs a{x + (xp ? r0 * k : r0 * ldx), ldx, (int)std::min(kPassRows, m - r0), w, k, n,
+               y + (yp ? r0 * n : r0 * ldy), ldy, yp ? 1 : 0, nullptr, nullptr, 0};
+    const int st = epilogue == kSiluMul       ? dispatch<kSiluMul>(a, c, layout, s)
+                   : epilogue == kAddResidual ? dispatch<kAddResidual>(a, c, layout, s)
+                                              : dispatch<kStore>(a, c, layout, s);
+    if (st) return st;
+  }
+  return OXR_OK;
 }
 
 int gemm_partial_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16* w, int64_t k, int64_t n,
@@ -957,8 +971,13 @@ int gemm_partial_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16
   const LaunchConfig c = choose_config(n, k, true);
   OXR_RETURN_IF(k_splits != c.k_splits, OXR_ERR_INVALID_ARG);
   if (m == 0) return OXR_OK;
-  GemmArgs a{x, ldx, (int)m, w, k, n, nullptr, 0, 0, nullptr, partials};
-  return dispatch<kPartial>(a, c, !packed ? kRowMajor : (xp ? kPackedWX : kPackedW), (hipStream_t)stream);
+  for (int64_t r0 = 0; r0 < m; r0 += kPassRows) {
+    GemmArgs a{x + (xp ? r0 * k : r0 * ldx), ldx, (int)std::min(kPassRows, m - r0), w, k, n, nullptr, 0, 0, nullptr,
+               partials + r0 * n, m};
+    const int st = dispatch<kPartial>(a, c, !packed ? kRowMajor : (xp ? kPackedWX : kPackedW), (hipStream_t)stream);
+    if (st) return st;
+  }
+  return OXR_OK;
 }
 
 int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
@@ -1000,7 +1019,7 @@ int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int
                     : launch_lm_head_lds_k<2, true>(hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits,
                                                     best, num_best, s);
   } else {
-    GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, 0, best, nullptr};
+    GemmArgs a{hidden, hidden_size, (int)m, weight, hidden_size, vocab, logits, vocab, 0, best, nullptr, 0};
     const LaunchConfig c = choose_config(vocab, hidden_size, false);
     num_best = (int)((vocab + 16 * c.na - 1) / (16 * c.na));
     st = dispatch<kArgmax>(a, c, packed ? kPackedW : kRowMajor, s);

@@ -48,7 +48,6 @@ namespace oxr {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kRows = 16;  // query rows per (sequence, kv head): one MFMA tile
 constexpr uint32_t kBf16One = 0x3f80u;
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -117,9 +116,12 @@ __device__ __forceinline__ uint32_t* out_vec(bf16_t* out, int64_t tok, int64_t c
   return reinterpret_cast<uint32_t*>(out + (packed ? packed_offset(tok, col, row_len) : tok * row_len + col));
 }
 
-constexpr int kWaves = 8;          // waves per workgroup
+constexpr int kWaves = 8;            // waves per workgroup
 constexpr int kMaxSpanPages = 4096;  // page-table entries of one split, staged in LDS
-constexpr int kMaxNew = 8;           // new tokens per sequence (S) of the fused kernel
+constexpr int kMaxRowTiles = 2;      // 16-row MFMA tiles of query rows per (sequence, kv head)
+constexpr int kPartRows = 16 * kMaxRowTiles;  // row stride of the split partials
+constexpr int kMaxNew = 16;          // new tokens per sequence (S) of the fused kernel
+constexpr int kJobSlots = 64 * kWaves / 16;   // 16-lane row jobs per round of the fused prologue
 
 // Inputs of the fused q/k norm + RoPE + KV store (oxr_qk_norm_rope_paged_extend).
 struct RopeArgs {
@@ -142,18 +144,24 @@ struct RopeArgs {
 // workgroup whose key range holds their positions, before any wave reads them;
 // otherwise q is read as given.  The caches are plain (not restrict) pointers
 // because the fused kernel writes the rows it later reads.
-template <bool kFused, int HPW>
+// NT: 16-row tiles of query rows (R = S * H / KV <= 16 * NT); every pair of keys
+// is multiplied by each tile, and the V^T fragments are shared by the tiles.
+// JR: rounds of the fused prologue's 32 row jobs (HPW * (R + 2 S) <= 32 * JR).
+template <bool kFused, int HPW, int NT, int JR>
 __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const bf16_t* __restrict__ q, const bf16_t* k_cache, const bf16_t* v_cache, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ block_table, int64_t table_stride, int S, int H, int KV, int log2_bs,
     int64_t num_blocks, float scale_log2, int max_seq_len, int splits, float* __restrict__ part_o,
     float* __restrict__ part_ml, bf16_t* __restrict__ out, int out_packed, RopeArgs ra) {
   constexpr int kStreams = kWaves / HPW;  // waves per kv head
-  __shared__ float s_o[kWaves][kRows][kD];
-  __shared__ u32x4 s_q[kFused ? HPW : 1][kFused ? kRows : 1][kD / 8];
+  // Two row tiles' q fragments (32 registers) would not fit next to two tiles'
+  // accumulators and the two pair buffers: with NT = 2 the MFMAs read them from LDS.
+  constexpr bool kQinLds = NT == 2;
+  __shared__ float s_o[kWaves][16][kD];   // one row tile's per-wave results at a time
+  __shared__ u32x4 s_q[kFused || kQinLds ? HPW : 1][kFused || kQinLds ? 16 * NT : 1][kD / 8];
   __shared__ u32x4 s_newk[kFused ? HPW : 1][kFused ? kMaxNew : 1][kD / 8];
   __shared__ u32x4 s_newv[kFused ? HPW : 1][kFused ? kMaxNew : 1][kD / 8];
-  __shared__ float s_m[kWaves][kRows], s_l[kWaves][kRows];
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ int s_pages[kMaxSpanPages];
 
   const int split = blockIdx.x, b = blockIdx.z;
@@ -166,38 +174,51 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   const int hs = wave % HPW, stream = wave / HPW;
   const int kvh = (int)blockIdx.y * HPW + hs;
 
-  // Fused: HPW * (R + 2S) <= 32 jobs of one 128-element row on 16 lanes --
-  // per head slot, q rows [0, R), then the K rows and the V rows of the S new
-  // tokens.  Lanes without a job redo job 0 (every lane must take part in the
-  // norm's exchanges) and store nothing.  Their loads go out first: none
-  // depends on the context length.
-  const int f_s16 = tid & 15, f_job = tid >> 4;
+  // Fused: HPW * (R + 2S) row jobs of one 128-element row each, on 16 lanes, in
+  // JR rounds of 32 -- per head slot, q rows [0, R), then the K rows and the V
+  // rows of the S new tokens.  Lanes without a job redo job 0 (every lane must
+  // take part in the norm's exchanges) and store nothing.  Their loads go out
+  // first: none depends on the context length.
+  const int f_s16 = tid & 15;
   const int f_per_head = R + 2 * S;
-  const bool f_valid = f_job < HPW * f_per_head;
-  int f_hs = 0, f_jj = 0, f_ss = 0;
-  int64_t f_trow = 0, f_slot = -1;
-  u32x4 f_raw = {0u, 0u, 0u, 0u}, f_w8 = {0u, 0u, 0u, 0u};
+  bool f_valid[JR];
+  int f_hs[JR], f_jj[JR], f_ss[JR];
+  int64_t f_trow[JR], f_slot[JR];
+  u32x4 f_raw[JR], f_w8[JR];
+#pragma unroll
+  for (int jr = 0; jr < JR; ++jr) {
+    f_valid[jr] = false;
+    f_hs[jr] = f_jj[jr] = f_ss[jr] = 0;
+    f_trow[jr] = 0;
+    f_slot[jr] = -1;
+    f_raw[jr] = f_w8[jr] = u32x4{0u, 0u, 0u, 0u};
+  }
   if constexpr (kFused) {
-    const int jv = f_valid ? f_job : 0;
-    f_hs = jv / f_per_head;
-    f_jj = jv % f_per_head;
-    const int kvh_j = (int)blockIdx.y * HPW + f_hs;
-    int head;
-    if (f_jj < R) {
-      f_ss = f_jj / G;
-      head = kvh_j * G + f_jj % G;
-    } else if (f_jj < R + S) {
-      f_ss = f_jj - R;
-      head = H + kvh_j;
-    } else {
-      f_ss = f_jj - R - S;
-      head = H + KV + kvh_j;
+#pragma unroll
+    for (int jr = 0; jr < JR; ++jr) {
+      const int job = (tid >> 4) + kJobSlots * jr;
+      f_valid[jr] = job < HPW * f_per_head;
+      const int jv = f_valid[jr] ? job : 0;
+      f_hs[jr] = jv / f_per_head;
+      f_jj[jr] = jv % f_per_head;
+      const int kvh_j = (int)blockIdx.y * HPW + f_hs[jr];
+      int head;
+      if (f_jj[jr] < R) {
+        f_ss[jr] = f_jj[jr] / G;
+        head = kvh_j * G + f_jj[jr] % G;
+      } else if (f_jj[jr] < R + S) {
+        f_ss[jr] = f_jj[jr] - R;
+        head = H + kvh_j;
+      } else {
+        f_ss[jr] = f_jj[jr] - R - S;
+        head = H + KV + kvh_j;
+      }
+      const int64_t tok = (int64_t)b * S + f_ss[jr];
+      f_raw[jr] = ld128(ra.qkv + (tok * (H + 2 * KV) + head) * kD + f_s16 * 8);
+      f_w8[jr] = ld128((f_jj[jr] < R ? ra.q_weight : ra.k_weight) + f_s16 * 8);
+      f_slot[jr] = ra.slots[tok];
+      f_trow[jr] = ra.positions[tok];
     }
-    const int64_t tok = (int64_t)b * S + f_ss;
-    f_raw = ld128(ra.qkv + (tok * (H + 2 * KV) + head) * kD + f_s16 * 8);
-    f_w8 = ld128((f_jj < R ? ra.q_weight : ra.k_weight) + f_s16 * 8);
-    f_slot = ra.slots[tok];
-    f_trow = ra.positions[tok];
   }
 
   const int L = min(seq_lens[b], max_seq_len);  // max_seq_len <= table span, checked on the host
@@ -229,7 +250,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   // (Issued by every wave -- a wave without pairs reads a valid row it never
   // uses -- so that no branch blurs the wait counts that follow.)
   PairRegs kv_a, kv_b;
-  u32x4 f_c8 = {0u, 0u, 0u, 0u}, f_s8 = {0u, 0u, 0u, 0u};
+  u32x4 f_c8[JR], f_s8[JR];
   {
     const int Lc = L > 0 ? L : 1;  // an empty context still addresses key 0
     const int tile0 = min(t_first, Lc - 1), tile1 = min(t_first + 16, Lc - 1);
@@ -239,10 +260,14 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const int64_t blk1 = e1 < 0 ? 0 : (e1 >= nb ? nb - 1 : e1);
     // Fused: the RoPE row of each new token's position, requested while the
     // first pair's page numbers are on their way.
-    if constexpr (kFused) {
-      f_trow = f_trow < 0 ? 0 : (f_trow >= ra.table_rows ? ra.table_rows - 1 : f_trow);
-      f_c8 = ld128(ra.cos_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
-      f_s8 = ld128(ra.sin_table + f_trow * (kD / 2) + (f_s16 & 7) * 8);
+#pragma unroll
+    for (int jr = 0; jr < JR; ++jr) {
+      f_c8[jr] = f_s8[jr] = u32x4{0u, 0u, 0u, 0u};
+      if constexpr (kFused) {
+        const int64_t row = f_trow[jr] < 0 ? 0 : (f_trow[jr] >= ra.table_rows ? ra.table_rows - 1 : f_trow[jr]);
+        f_c8[jr] = ld128(ra.cos_table + row * (kD / 2) + (f_s16 & 7) * 8);
+        f_s8[jr] = ld128(ra.sin_table + row * (kD / 2) + (f_s16 & 7) * 8);
+      }
     }
     load_pair(kv_a, k_cache, v_cache, blk0, blk1, t_first, Lc, kvh, KV, log2_bs, r, g);
   }
@@ -257,39 +282,53 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 
   if constexpr (kFused) {
     // The new tokens' rows (see the top of the kernel for the job layout).
-    const u32x4 normed = norm_rope_16v(f_raw, f_w8, f_c8, f_s8, ra.eps, f_s16);
-    if (f_valid && f_jj < R) {
-      s_q[f_hs][f_jj][f_s16] = normed;
-    } else if (f_valid) {
-      // Kept in LDS for this workgroup's own reads of the new rows, and
-      // written to the cache by the workgroup whose keys hold the token's
-      // position (each row stored once; nothing in this launch reads it back
-      // from memory, so the stores need not complete before the loop).
-      const bool is_k = f_jj < R + S;
-      if (is_k) s_newk[f_hs][f_ss][f_s16] = normed;
-      else s_newv[f_hs][f_ss][f_s16] = f_raw;
-      const int pos = L - S + f_ss;
-      if (pos >= t_begin && pos < t_end && f_slot >= 0 && f_slot < ra.num_slots) {
-        const int kvh_j = (int)blockIdx.y * HPW + f_hs;
-        bf16_t* dst = (is_k ? ra.k_store : ra.v_store) + (f_slot * KV + kvh_j) * kD + f_s16 * 8;
-        st128(dst, is_k ? normed : f_raw);
+#pragma unroll
+    for (int jr = 0; jr < JR; ++jr) {
+      const u32x4 normed = norm_rope_16v(f_raw[jr], f_w8[jr], f_c8[jr], f_s8[jr], ra.eps, f_s16);
+      if (f_valid[jr] && f_jj[jr] < R) {
+        s_q[f_hs[jr]][f_jj[jr]][f_s16] = normed;
+      } else if (f_valid[jr]) {
+        // Kept in LDS for this workgroup's own reads of the new rows, and
+        // written to the cache by the workgroup whose keys hold the token's
+        // position (each row stored once; nothing in this launch reads it back
+        // from memory, so the stores need not complete before the loop).
+        const bool is_k = f_jj[jr] < R + S;
+        if (is_k) s_newk[f_hs[jr]][f_ss[jr]][f_s16] = normed;
+        else s_newv[f_hs[jr]][f_ss[jr]][f_s16] = f_raw[jr];
+        const int pos = L - S + f_ss[jr];
+        if (pos >= t_begin && pos < t_end && f_slot[jr] >= 0 && f_slot[jr] < ra.num_slots) {
+          const int kvh_j = (int)blockIdx.y * HPW + f_hs[jr];
+          bf16_t* dst = (is_k ? ra.k_store : ra.v_store) + (f_slot[jr] * KV + kvh_j) * kD + f_s16 * 8;
+          st128(dst, is_k ? normed : f_raw[jr]);
+        }
       }
     }
   }
 
-  u32x4 qf[4];
-  int qpos = -1;  // absolute position of row r; keys after it are masked
-  if (r < R) {
-    const int s = r / G, hh = r % G;
-    if constexpr (!kFused) {
-      const bf16_t* src = q + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + 8 * g;
+  // Query row 16t + r of tile t: token (16t + r) / G, head (16t + r) % G of this kv head.
+  u32x4 qf[NT][4];
+  int qpos[NT];  // absolute position of the row; keys after it are masked
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qf[i] = ld128(src + 32 * i);
+  for (int t = 0; t < NT; ++t) {
+    const int rr = 16 * t + r;
+    qpos[t] = -1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[t][i] = u32x4{0u, 0u, 0u, 0u};
+    if (rr < R) {
+      const int s = rr / G, hh = rr % G;
+      if constexpr (!kFused) {
+        const bf16_t* src = q + (((int64_t)b * S + s) * H + kvh * G + hh) * kD + 8 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qf[t][i] = ld128(src + 32 * i);
+      }
+      qpos[t] = L - S + s;
     }
-    qpos = L - S + s;
-  } else {
+    if constexpr (kQinLds && !kFused) {
+      if (stream == 0) {  // wave-uniform: one wave per head stages its rows (zeros past R)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qf[i] = u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 4; ++i) s_q[hs][rr][4 * i + g] = qf[t][i];
+      }
+    }
   }
   const u32x4 sel_lo = selector(r, g, 0), sel_hi = selector(r, g, 16);
   // LDS (s_pages; fused: s_q and the new K/V rows) is complete; global loads
@@ -297,19 +336,28 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  if constexpr (kFused) {
-    if (r < R) {
+  if constexpr (kFused && !kQinLds) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qf[i] = s_q[hs][r][4 * i + g];
+    for (int t = 0; t < NT; ++t) {
+      if (16 * t + r < R) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qf[t][i] = s_q[hs][16 * t + r][4 * i + g];
+      }
     }
   }
 
-  // Running row maximum of the raw scores (m_run) and the same in the exp2
-  // domain (mc_run = m_run * scale * log2 e; 0 while every key is masked).
-  float m_run = -INFINITY, mc_run = 0.f, l_run = 0.f;
-  f32x4 o[8];
+  // Per row tile: running row maximum of the raw scores (m_run) and the same in
+  // the exp2 domain (mc_run = m_run * scale * log2 e; 0 while every key is masked).
+  float m_run[NT], mc_run[NT], l_run[NT];
+  f32x4 o[NT][8];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NT; ++t) {
+    m_run[t] = -INFINITY;
+    mc_run[t] = 0.f;
+    l_run[t] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto step = [&](PairRegs& cur, const int t0) {
     if constexpr (kFused) {
@@ -326,48 +374,58 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         }
       }
     }
-    // Raw scores of keys t0 + 16p + 4g + j for query row r.
-    float sv[8];
+    u32x4 pb[NT];
+    if constexpr (kQinLds) __asm__ __volatile__("" ::: "memory");  // keep the q reads below in the loop
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NT; ++t) {
+      // Raw scores of keys t0 + 16p + 4g + j for query row 16t + r (rows past R
+      // hold zeros in s_q and are fully masked).
+      float sv[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc = mfma_16x16x32(cur.k[p][i], qf[i], acc);
+      for (int p = 0; p < 2; ++p) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sv[4 * p + j] = acc[j];
+        for (int i = 0; i < 4; ++i)
+          acc = mfma_16x16x32(cur.k[p][i], kQinLds ? s_q[hs][16 * t + r][4 * i + g] : qf[t][i], acc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sv[4 * p + j] = acc[j];
+      }
+      if (t0 + 31 > L - S) {  // wave-uniform: only pairs at the causal frontier need the mask
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (t0 + 16 * (e >> 2) + 4 * g + (e & 3) > qpos[t]) sv[e] = -INFINITY;
+      }
+      float mx =
+          fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      mx = xor32_max(xor16_max(mx));
+      // Probabilities exp2(s * c - m * c) against the running row maximum m;
+      // the accumulators are rescaled only when some row's maximum moved (when
+      // it did not, the factor is exactly 1).
+      const bool moved = mx > m_run[t];
+      if (__builtin_amdgcn_ballot_w64(moved)) {
+        const float m_new = moved ? mx : m_run[t];
+        const float mc_new = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+        // (Nothing is accumulated while the maximum is -inf: factor 0, never inf.)
+        const float alpha =
+            !moved ? 1.0f : (m_run[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc_run[t] - mc_new));
+        l_run[t] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[t][dt] *= alpha;
+        m_run[t] = m_new;
+        mc_run[t] = mc_new;
+      }
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], scale_log2, -mc_run[t]));
+        l_run[t] += pv[e];
+      }
+      pb[t] = u32x4{pack_bf_hw(pv[0], pv[1]), pack_bf_hw(pv[2], pv[3]), pack_bf_hw(pv[4], pv[5]),
+                    pack_bf_hw(pv[6], pv[7])};
     }
-    if (t0 + 31 > L - S) {  // wave-uniform: only pairs at the causal frontier need the mask
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (t0 + 16 * (e >> 2) + 4 * g + (e & 3) > qpos) sv[e] = -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-    mx = xor32_max(xor16_max(mx));
-    // Probabilities exp2(s * c - m * c) against the running row maximum m;
-    // the accumulators are rescaled only when some row's maximum moved (when
-    // it did not, the factor is exactly 1).
-    const bool moved = mx > m_run;
-    if (__builtin_amdgcn_ballot_w64(moved)) {
-      const float m_new = moved ? mx : m_run;
-      const float mc_new = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-      // (Nothing is accumulated while the maximum is -inf: factor 0, never inf.)
-      const float alpha = !moved ? 1.0f : (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc_run - mc_new));
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-      m_run = m_new;
-      mc_run = mc_new;
-    }
-    float pv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], scale_log2, -mc_run));
-      l_run += pv[e];
-    }
-    const u32x4 pb = {pack_bf_hw(pv[0], pv[1]), pack_bf_hw(pv[2], pv[3]), pack_bf_hw(pv[4], pv[5]),
-                      pack_bf_hw(pv[6], pv[7])};
 
-    // V^T fragments: dims 32c + [0, 16) and 32c + [16, 32) of both tiles.
+    // V^T fragments: dims 32c + [0, 16) and 32c + [16, 32) of both key tiles,
+    // each multiplied into every row tile.
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
@@ -379,7 +437,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         const u32x4 a = {pack_hi16(v0[0], v0[1]), pack_hi16(v0[2], v0[3]), pack_hi16(v1[0], v1[1]),
                          pack_hi16(v1[2], v1[3])};
         const int dt = 2 * c + half;
-        o[dt] = mfma_16x16x32(a, pb, o[dt]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o[t][dt] = mfma_16x16x32(a, pb[t], o[t][dt]);
       }
     }
   };
@@ -404,43 +463,49 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     }
   }
 
-  // Merge each head's kStreams waves on chip.
-  const float l_tot = xor32_sum(xor16_sum(l_run));
+  // Merge each head's kStreams waves on chip, one row tile at a time.
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[dt];
-  if (g == 0) {
-    s_m[wave][r] = m_run == -INFINITY ? -INFINITY : mc_run;
-    s_l[wave][r] = l_tot;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < HPW * R * (kD / 4); idx += 64 * kWaves) {
-    const int ho = idx / (R * (kD / 4)), rr = (idx / (kD / 4)) % R, d0 = (idx % (kD / 4)) * 4;
-    const int kvh_o = (int)blockIdx.y * HPW + ho;
-    const int64_t unit0 = ((int64_t)b * KV + kvh_o) * splits;
-    float mmax = -INFINITY;
+  for (int t = 0; t < NT; ++t) {
+    const float l_tot = xor32_sum(xor16_sum(l_run[t]));
+    if (t > 0) __syncthreads();  // the previous tile's merge has read s_o, s_m, s_l
 #pragma unroll
-    for (int k = 0; k < kStreams; ++k) mmax = fmaxf(mmax, s_m[ho + HPW * k][rr]);
-    const float mu = (mmax == -INFINITY) ? 0.f : mmax;
-    float l = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < kStreams; ++k) {
-      const int w = ho + HPW * k;
-      const float wt = exp2f(s_m[w][rr] - mu);
-      l += s_l[w][rr] * wt;
-      acc += *reinterpret_cast<const f32x4*>(&s_o[w][rr][d0]) * wt;
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[t][dt];
+    if (g == 0) {
+      s_m[wave][r] = m_run[t] == -INFINITY ? -INFINITY : mc_run[t];
+      s_l[wave][r] = l_tot;
     }
-    if (single) {
-      const float inv = l > 0.f ? 1.0f / l : 0.f;
-      const int s = rr / G, hh = rr % G;
-      uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh_o * G + hh) * kD + d0, H * kD, out_packed);
-      dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
-      dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
-    } else {
-      f32x4* const po = reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kRows + rr) * kD + d0);
-      if (OXR_NT_PART) __builtin_nontemporal_store(acc, po);
-      else *po = acc;
-      if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + ((unit0 + split) * kRows + rr) * 2) = f32x2{mmax, l};
+    __syncthreads();
+    const int rows = min(16, R - 16 * t);
+    for (int idx = tid; idx < HPW * rows * (kD / 4); idx += 64 * kWaves) {
+      const int ho = idx / (rows * (kD / 4)), rl = (idx / (kD / 4)) % rows, d0 = (idx % (kD / 4)) * 4;
+      const int rr = 16 * t + rl;
+      const int kvh_o = (int)blockIdx.y * HPW + ho;
+      const int64_t unit0 = ((int64_t)b * KV + kvh_o) * splits;
+      float mmax = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < kStreams; ++k) mmax = fmaxf(mmax, s_m[ho + HPW * k][rl]);
+      const float mu = (mmax == -INFINITY) ? 0.f : mmax;
+      float l = 0.f;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < kStreams; ++k) {
+        const int w = ho + HPW * k;
+        const float wt = exp2f(s_m[w][rl] - mu);
+        l += s_l[w][rl] * wt;
+        acc += *reinterpret_cast<const f32x4*>(&s_o[w][rl][d0]) * wt;
+      }
+      if (single) {
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        const int s = rr / G, hh = rr % G;
+        uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh_o * G + hh) * kD + d0, H * kD, out_packed);
+        dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
+        dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
+      } else {
+        f32x4* const po = reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kPartRows + rr) * kD + d0);
+        if (OXR_NT_PART) __builtin_nontemporal_store(acc, po);
+        else *po = acc;
+        if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + ((unit0 + split) * kPartRows + rr) * 2) = f32x2{mmax, l};
+      }
     }
   }
 }
@@ -448,11 +513,12 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 // Merge of the context splits of every (sequence, kv head): one workgroup per
 // pair, one thread per 4 output dims of a row.  Sequences whose context fitted
 // one split were already stored by the main kernel.
-__global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(const float* __restrict__ part_o,
-                                                                          const float* __restrict__ part_ml,
-                                                                          const int32_t* __restrict__ seq_lens, int S,
-                                                                          int H, int KV, int max_seq_len, int splits,
-                                                                          bf16_t* __restrict__ out, int out_packed) {
+__global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(const float* __restrict__ part_o,
+                                                                              const float* __restrict__ part_ml,
+                                                                              const int32_t* __restrict__ seq_lens,
+                                                                              int S, int H, int KV, int max_seq_len,
+                                                                              int splits, bf16_t* __restrict__ out,
+                                                                              int out_packed) {
   constexpr int kChunk = 8;  // splits whose partials are requested together
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int G = H / KV;
@@ -469,8 +535,8 @@ __global__ __launch_bounds__(kRows * kD / 4) void paged_extend_merge_kernel(cons
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
       const int64_t u = unit0 + min(c0 + j, splits - 1);
-      ml[j] = *reinterpret_cast<const f32x2*>(part_ml + (u * kRows + rr) * 2);
-      v[j] = *reinterpret_cast<const f32x4*>(part_o + (u * kRows + rr) * kD + d0);
+      ml[j] = *reinterpret_cast<const f32x2*>(part_ml + (u * kPartRows + rr) * 2);
+      v[j] = *reinterpret_cast<const f32x4*>(part_o + (u * kPartRows + rr) * kD + d0);
     }
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
@@ -518,17 +584,23 @@ int splits_for(int32_t batch, int32_t num_kv_heads, int hpw, int32_t max_seq_len
 // kv heads per workgroup: two heads read 512-byte slices of each token row
 // together (the heads of a row are adjacent) -- measured 1 us faster per
 // launch than one head at the verify shape; four heads (16 splits) were 3 us
-// slower.  The fused kernel's row jobs must fit one per 16-lane group; the
-// unfused kernel makes the same choice, so that both split the context the
-// same way and give the same bits.
+// slower.  Two heads only when the fused kernel's row jobs then fit one round
+// of 32 16-lane groups; the unfused kernel makes the same choice, so that both
+// split the context the same way and give the same bits.
 int pick_hpw(int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads) {
   const int jobs_per_head = tokens_per_seq * (num_heads / num_kv_heads + 2);
   for (int hpw : {2, 1}) {
     if (OXR_ATTN_HPW != 0 && hpw != OXR_ATTN_HPW) continue;
-    if (num_kv_heads % hpw != 0 || hpw * jobs_per_head > 32) continue;
+    if (num_kv_heads % hpw != 0 || hpw * jobs_per_head > kJobSlots) continue;
     return hpw;
   }
   return 1;
+}
+
+// Rounds of 32 row jobs the fused prologue needs (at most 2).
+int job_rounds(int hpw, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads) {
+  const int jobs = hpw * tokens_per_seq * (num_heads / num_kv_heads + 2);
+  return (jobs + kJobSlots - 1) / kJobSlots;
 }
 
 }  // namespace
@@ -540,12 +612,15 @@ extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv
   // Partials of the largest (batch' * KV * splits) over any head grouping and any batch' <= batch:
   // smaller batches split their contexts further, and a workspace sized for a batch serves every
   // smaller one.
+  // (A launch with one split stores its output directly and needs none.)
   size_t units = 0;
   for (int32_t bb = 1; bb <= batch; ++bb)
     for (int hpw : {1, 2})
-      if (num_kv_heads % hpw == 0)
-        units = std::max(units, (size_t)bb * num_kv_heads * splits_for(bb, num_kv_heads, hpw, max_seq_len));
-  return units * kRows * (kD + 2) * sizeof(float);
+      if (num_kv_heads % hpw == 0) {
+        const int splits = splits_for(bb, num_kv_heads, hpw, max_seq_len);
+        if (splits > 1) units = std::max(units, (size_t)bb * num_kv_heads * splits);
+      }
+  return units * kPartRows * (kD + 2) * sizeof(float);
 }
 
 namespace oxr {
@@ -562,14 +637,14 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
                     table_stride < 0 || max_seq_len <= 0,
                 OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(head_dim != kD || num_heads % num_kv_heads != 0, OXR_ERR_UNSUPPORTED);
-  OXR_RETURN_IF(tokens_per_seq * (num_heads / num_kv_heads) > kRows, OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(tokens_per_seq * (num_heads / num_kv_heads) > kPartRows, OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(block_size < 16 || (block_size & (block_size - 1)) != 0, OXR_ERR_UNSUPPORTED);
   // Contexts are clamped to max_seq_len, so every key visited maps to a table entry.
   OXR_RETURN_IF((int64_t)max_seq_len > table_stride * block_size, OXR_ERR_INVALID_ARG);
   if (batch == 0) return OXR_OK;
   OXR_RETURN_IF((!ra && !q) || !k_cache || !v_cache || !seq_lens || !block_table || !out, OXR_ERR_INVALID_ARG);
   const size_t need = oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len);
-  OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
+  OXR_RETURN_IF((need > 0 && !workspace) || workspace_bytes < need, OXR_ERR_WORKSPACE);
   OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535 || num_blocks > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
   const int hpw = pick_hpw(tokens_per_seq, num_heads, num_kv_heads);
   const int splits = splits_for(batch, num_kv_heads, hpw, max_seq_len);
@@ -581,7 +656,7 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   int log2_bs = 0;
   while ((1 << log2_bs) < block_size) ++log2_bs;
   float* part_o = static_cast<float*>(workspace);
-  float* part_ml = part_o + (size_t)batch * num_kv_heads * splits * kRows * kD;
+  float* part_ml = part_o + (size_t)batch * num_kv_heads * splits * kPartRows * kD;
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(splits, num_kv_heads / hpw, batch), block(64 * kWaves);
   const RopeArgs rope = ra ? *ra : RopeArgs{};
@@ -590,12 +665,25 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
                        table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
                        max_seq_len, splits, part_o, part_ml, out, out_packed, rope);
   };
+  const int nt = tokens_per_seq * (num_heads / num_kv_heads) > 16 ? 2 : 1;
   if (ra) {
-    if (hpw == 2) launch(paged_extend_kernel<true, 2>);
-    else launch(paged_extend_kernel<true, 1>);
+    const int jr = job_rounds(hpw, tokens_per_seq, num_heads, num_kv_heads);  // 1 or 2, checked by the caller
+    switch ((hpw - 1) * 4 + (nt - 1) * 2 + (jr - 1)) {
+      case 0: launch(paged_extend_kernel<true, 1, 1, 1>); break;
+      case 1: launch(paged_extend_kernel<true, 1, 1, 2>); break;
+      case 2: launch(paged_extend_kernel<true, 1, 2, 1>); break;
+      case 3: launch(paged_extend_kernel<true, 1, 2, 2>); break;
+      case 4: launch(paged_extend_kernel<true, 2, 1, 1>); break;
+      case 6: launch(paged_extend_kernel<true, 2, 2, 1>); break;
+      default: return OXR_ERR_UNSUPPORTED;  // two heads are only chosen when one round holds their jobs
+    }
   } else {
-    if (hpw == 2) launch(paged_extend_kernel<false, 2>);
-    else launch(paged_extend_kernel<false, 1>);
+    switch ((hpw - 1) * 2 + (nt - 1)) {
+      case 0: launch(paged_extend_kernel<false, 1, 1, 1>); break;
+      case 1: launch(paged_extend_kernel<false, 1, 2, 1>); break;
+      case 2: launch(paged_extend_kernel<false, 2, 1, 1>); break;
+      default: launch(paged_extend_kernel<false, 2, 2, 1>); break;
+    }
   }
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;
@@ -631,9 +719,9 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
                                              size_t workspace_bytes, oxr_stream_t stream) {
   using namespace oxr;
   OXR_RETURN_IF(num_slots < 0, OXR_ERR_INVALID_ARG);
-  // One 16-lane job per q row and per new K and V row: 32 per workgroup.
+  // One 16-lane job per q row and per new K and V row, in at most two rounds of 32.
   OXR_RETURN_IF(num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
-                    (tokens_per_seq > kMaxNew || tokens_per_seq * (num_heads / num_kv_heads + 2) > 32),
+                    (tokens_per_seq > kMaxNew || tokens_per_seq * (num_heads / num_kv_heads + 2) > 2 * kJobSlots),
                 OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(batch > 0 && (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || table_rows <= 0 ||
                               !positions || !slots),
@@ -658,7 +746,11 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
 namespace oxr {
 namespace {
 
-constexpr size_t kScratchBytes = (size_t)32 << 20;
+// Every shape fits: a launch splits its contexts only while its workgroup units
+// (batch * KV / HPW) number fewer than 256, into ceil(256 / units) splits, so
+// the partials of any launch cover at most HPW * max_u(u * ceil(256 / u)) =
+// 2 * 510 < 1024 (sequence, kv head, split) units of kPartRows x (kD + 2) fp32.
+constexpr size_t kScratchBytes = (size_t)1024 * kPartRows * (kD + 2) * sizeof(float);  // 16.25 MiB
 constexpr int kScratchMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 

@@ -90,7 +90,7 @@ def pack_weight(w: torch.Tensor) -> PackedMatrix:
 
 EPI_STORE, EPI_SILU_MUL, EPI_ADD_RESIDUAL = 0, 1, 3
 X_PACKED, Y_PACKED = 1, 2  # OXR_GEMM_X_PACKED, OXR_GEMM_Y_PACKED
-MAX_ROWS = 64  # token rows per launch; larger inputs are processed in slices
+MAX_ROWS = 256  # token rows per call (the kernels take 64 per launch over the same weight); more are sliced
 
 
 def _tensor(a: Weight) -> torch.Tensor:
@@ -114,7 +114,7 @@ def _run(x: Rows, w: Weight, n: int, epilogue: int, y: Rows, device: torch.devic
     if isinstance(w, PackedMatrix):
         flags = (X_PACKED if isinstance(x, PackedMatrix) else 0) | (Y_PACKED if isinstance(y, PackedMatrix) else 0)
         if flags:
-            _lib.require(m <= MAX_ROWS, "packed rows: at most 64 per call")
+            _lib.require(m <= MAX_ROWS, f"packed rows: at most {MAX_ROWS} per call")
         ldx = 0 if isinstance(x, PackedMatrix) else x.stride(0)
         ldy = 0 if isinstance(y, PackedMatrix) else y.stride(0)
         for start in range(0, m, MAX_ROWS):
@@ -181,7 +181,7 @@ def linear_partial(x: Rows, w: Weight, partials: torch.Tensor) -> int:
     ``partials[:splits, :m, :n]``; returns the number of slices."""
     device = _check(x, w, "linear_partial")
     m, (n, k) = x.shape[0], w.shape
-    _lib.require(m <= MAX_ROWS, "linear_partial: at most 64 rows")
+    _lib.require(m <= MAX_ROWS, f"linear_partial: at most {MAX_ROWS} rows")
     splits = partial_splits(n, k)
     _lib.require(partials.dtype == torch.float32 and partials.is_contiguous() and partials.numel() >= splits * m * n,
                  "linear_partial: partials must be contiguous fp32 with room for splits * m * n")

@@ -86,3 +86,30 @@ def test_entry_points_reject_bad_arguments_before_launch() -> None:
     assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 64, 0, 4096, 0, 2, None) == -2
     assert lib.oxr_gemm_bf16_packed(16, 128, 4, 32, 128, 128, 3, 4096, 0, 2, None) == -2
     assert lib.oxr_gemm_bf16_partial_packed(16, 0, 4, 32, 128, 64, 4096, 1, 2, None) == -1  # y flag on partials
+
+
+def test_static_scratch_holds_every_attention_workspace() -> None:
+    """Host-side sizing only (no GPU call): the fused attention's allocation-free entry point keeps its
+    split partials in a static array that must hold the workspace of every shape the workspace entry
+    point takes -- any batch, kv-head count and context bound."""
+    handle = pkg("_lib").lib()
+    limit = handle.oxr_static_scratch_bytes()
+    worst = 0
+    for kv in (1, 2, 3, 4, 8, 16, 32, 64):
+        for batch in list(range(1, 130)) + [255, 256, 257, 511, 512, 4096]:
+            for max_len in (16, 255, 256, 257, 1000, 4096, 16384, 1 << 20):
+                worst = max(worst, handle.oxr_paged_extend_workspace_bytes(batch, kv, max_len))
+    assert 0 < worst <= limit, (worst, limit)
+
+
+def test_build_rejects_kernels_with_scratch() -> None:
+    """The build's guard reads the compiler's resource-usage remarks and names every kernel with
+    a nonzero ScratchSize."""
+    build = pkg("build")
+    remarks = (
+        "a.hip:1:1: remark: Function Name: k_clean [-Rpass-analysis=kernel-resource-usage]\n"
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]\n"
+        "a.hip:9:1: remark: Function Name: k_spills [-Rpass-analysis=kernel-resource-usage]\n"
+        "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 56 [-Rpass-analysis=kernel-resource-usage]\n"
+    )
+    assert build.scratch_users(remarks) == [("k_spills", 56)]

@@ -109,3 +109,23 @@ def test_workspace_sized_for_a_batch_serves_smaller_batches() -> None:
         fresh = attention.paged_extend(q, kc, vc, seq_t, table_t, max_seq_len=max_len)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), fresh.view(torch.int16)), f"batch {batch}"
+
+
+def test_reference_default_width_s9() -> None:
+    """The reference's default verify width: 1 + speculative_tokens = 9 tokens per sequence
+    (engine.py:121, 242-246) at 16/8 heads, so 18 query rows per kv head (two 16-row MFMA tiles),
+    config 3's contexts and pool, and the reference's block size 256."""
+    rng = np.random.default_rng(37)
+    seq_lens = rng.integers(2048, 8193, size=8)
+    announce("attention S=9, 16/8 heads", seq_lens.tolist())
+    _run(seq_lens, 9, 16, 8, 16, 65_536, seed=37)
+    announce("attention S=9, block 256")
+    _run([300, 9, 1000, 2600], 9, 16, 8, 256, 64, seed=38)
+
+
+@pytest.mark.parametrize("S,H,KV", [(16, 16, 8), (12, 8, 8), (5, 32, 8), (16, 16, 16)])
+def test_query_row_tiles(S, H, KV) -> None:
+    """Up to 32 query rows per kv head: 16 tokens x 2 heads (both tiles full), 12 x 1, 5 x 4 (20
+    rows), 16 tokens of MHA; contexts shorter than S, inside one split, and across splits."""
+    announce("attention row tiles", S, H, KV)
+    _run([S, S + 1, 700, 3000], S, H, KV, 16, 1024, seed=39 + S + H)

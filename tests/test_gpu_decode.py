@@ -7,7 +7,7 @@
   sequence (the oracle), within the tolerance of the end-to-end forward.
 - ``DecodeGraphs`` (decode_graph.py:33-119): graph replay gives exactly the eager decode's logits
   and ids, padded bucket rows touch only the scratch page, and batches past the largest bucket
-  return None.
+  return None; up to the engine's 256 running sequences (engine.py:111).
 """
 
 from __future__ import annotations
@@ -35,7 +35,8 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("seq_lens,block_size", [([1, 7, 16, 33, 300, 2049, 4100, 5], 16), ([1, 257, 900], 256)])
+@pytest.mark.parametrize("seq_lens,block_size", [([1, 7, 16, 33, 300, 2049, 4100, 5], 16), ([1, 257, 900], 256),
+                                                 (np.random.default_rng(256).integers(1, 2000, size=256).tolist(), 16)])
 def test_paged_decode_matches_oracle(seq_lens, block_size) -> None:
     rng = np.random.default_rng(len(seq_lens))
     B, H, KV = len(seq_lens), 16, 8
@@ -109,19 +110,24 @@ def test_decode_after_prefill_equals_full_sequence() -> None:
         assert (err.pow(2).sum() / want.pow(2).sum()).sqrt().item() < 2e-2
 
 
-def test_decode_graphs_match_eager_and_keep_padding_on_scratch() -> None:
+@pytest.mark.parametrize("max_batch,n,buckets", [(6, 3, [1, 2, 4, 6]),
+                                                  (256, 200, [1, 2, 4, 8, 16, 32, 64, 128, 192, 256])])
+def test_decode_graphs_match_eager_and_keep_padding_on_scratch(max_batch, n, buckets) -> None:
+    """n sequences replayed in the next bucket up (3 in the bucket of 4; 200 of the engine's up to
+    256 running sequences, engine.py:111, in the bucket of 256, 200 token rows through the
+    GEMMs)."""
     model, _ = _model(seed=22)
     rng = np.random.default_rng(22)
-    bs, num_blocks, width = 16, 64, 8
+    bs, width = 16, 8
+    num_blocks = 8 * n + 16
     cache = kv_cache.KVCache(SMALL.num_layers, SMALL.num_kv_heads, SMALL.head_dim, num_blocks, block_size=bs)
     g = torch.Generator(device="cuda").manual_seed(22)
     cache.k.copy_(torch.randn(cache.k.shape, generator=g, device="cuda").to(torch.bfloat16))
     cache.v.copy_(torch.randn(cache.v.shape, generator=g, device="cuda").to(torch.bfloat16))
-    announce("DecodeGraphs")
-    graphs = decode_graph.DecodeGraphs(model, cache, max_batch=6, max_positions=width * bs)
-    assert graphs.buckets == [1, 2, 4, 6]
+    announce("DecodeGraphs", max_batch, n)
+    graphs = decode_graph.DecodeGraphs(model, cache, max_batch=max_batch, max_positions=width * bs)
+    assert graphs.buckets == buckets
     pages = [p for p in range(num_blocks) if p != graphs.scratch_block]
-    n = 3  # replayed in the bucket of 4: one padded row
     lens = rng.integers(20, width * bs - 1, size=n)
     tables = [pages[8 * b : 8 * b + int(-(-(lens[b] + 1) // bs))] for b in range(n)]
     ids = rng.integers(0, SMALL.vocab_size, size=n).tolist()
@@ -158,11 +164,12 @@ def test_decode_graphs_match_eager_and_keep_padding_on_scratch() -> None:
     assert torch.equal(logits.view(torch.int16), want_logits.view(torch.int16))
     assert torch.equal(cache.k, after_k) and torch.equal(cache.v, after_v)
 
-    assert graphs.run([0] * 7, [0] * 7, [0] * 7, [1] * 7, [[0]] * 7) is None  # past the largest bucket
+    big = max_batch + 1
+    assert graphs.run([0] * big, [0] * big, [0] * big, [1] * big, [[0]] * big) is None  # past the largest bucket
 
 
 def test_decode_graphs_reject_batches_past_the_kernels() -> None:
     model, _ = _model(seed=23)
     cache = kv_cache.KVCache(SMALL.num_layers, SMALL.num_kv_heads, SMALL.head_dim, 4, block_size=16)
     with pytest.raises(ValueError):
-        decode_graph.DecodeGraphs(model, cache, max_batch=65, max_positions=64)
+        decode_graph.DecodeGraphs(model, cache, max_batch=257, max_positions=64)

@@ -329,3 +329,55 @@ def test_step_record_expands_to_padded_bucket() -> None:
     assert table[:bucket].tolist() == want
     with pytest.raises(ValueError):
         rec.write(ids, positions, slots, seq_lens, [[1] * (width + 1), [], []])  # page list wider than the table
+
+
+GQA16 = language.LanguageConfig(1024, 1536, 2, 16, 8, 128, 1e-6, 1e6, 1000)
+
+
+@pytest.mark.parametrize("n", [8, 5])
+def test_extend_graphs_reference_defaults(n) -> None:
+    """The engine's verify graphs at the reference's defaults (speculative_tokens = 8,
+    speculative_max_batch = 8: ExtendGraphs(max_batch=8, tokens_per_seq=9), engine.py:121-123,
+    242-246) on a 16/8-head model: 72 token rows through the GEMMs, 18 query rows per kv head.
+    The replay equals eager extend bit for bit (n = 5: padded in the bucket of 8), and its greedy
+    ids equal the oracle's wherever the oracle's top-2 margin is clear."""
+    rng = np.random.default_rng(40 + n)
+    model, cpu_w = _model(GQA16, seed=40)
+    bs, s = 16, 9
+    cache = _cache(GQA16, 512, bs, seed=41)
+    scratch = cache.allocate(1)[0]
+    announce("extend graphs S=9 capture", n)
+    graphs = decode_graph.ExtendGraphs(model, cache, max_batch=8, tokens_per_seq=s, max_positions=1024,
+                                       scratch_block=scratch)
+    assert graphs.buckets == [1, 2, 4, 8]
+    tables = [cache.allocate(int(rng.integers(8, 40))) for _ in range(n)]
+    seq_lens = [int(rng.integers(s, len(t) * bs)) for t in tables]
+    ids, positions, slots = [], [], []
+    for b in range(n):
+        for j in range(s):
+            pos = seq_lens[b] - s + j
+            ids.append(int(rng.integers(0, GQA16.vocab_size)))
+            positions.append(pos)
+            slots.append(kv_cache.slot_of(tables[b], pos, bs))
+    cpu_k, cpu_v = cache.k.cpu(), cache.v.cpu()
+    before_k, before_v = cache.k.clone(), cache.v.clone()
+    tokens = graphs.run(ids, positions, slots, seq_lens, tables).clone()
+    torch.cuda.synchronize()
+    after_k, after_v = cache.k.clone(), cache.v.clone()
+    # The graphs' table width (max_positions / block size): the same context split, so the same bits.
+    table = np.full((n, graphs.width), scratch, dtype=np.int32)
+    for b in range(n):
+        table[b, : len(tables[b])] = tables[b]
+    cache.k.copy_(before_k)
+    cache.v.copy_(before_v)
+    eb = language.ExtendBatch(torch.tensor(ids).cuda(), torch.tensor(positions).cuda(), torch.tensor(slots).cuda(),
+                              torch.tensor(seq_lens, dtype=torch.int32).cuda(), torch.from_numpy(table).cuda(), s)
+    eager = model.greedy(model.extend(eb, cache)).view(n, s)
+    torch.cuda.synchronize()
+    assert torch.equal(tokens, eager)
+    flat = lambda c: c.view(GQA16.num_layers, -1, GQA16.num_kv_heads, GQA16.head_dim)
+    assert torch.equal(flat(cache.k)[:, slots], flat(after_k)[:, slots])
+    assert torch.equal(flat(cache.v)[:, slots], flat(after_v)[:, slots])
+    hidden = oracle_decoder.extend(GQA16, cpu_w, torch.tensor(ids), torch.tensor(positions), torch.tensor(slots),
+                                   torch.tensor(seq_lens, dtype=torch.int32), torch.from_numpy(table), s, cpu_k, cpu_v)
+    _ids_agree(tokens.reshape(-1).cpu().numpy(), oracle_decoder.logits(cpu_w, hidden), margin_floor=0.1)

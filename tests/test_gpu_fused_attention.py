@@ -109,3 +109,18 @@ def test_eight_new_tokens_long_contexts() -> None:
 def test_single_sequence_many_splits() -> None:
     announce("fused attention B=1 (32 splits)")
     _case([5000], 4, 16, 8, 16, seed=13)
+
+
+@pytest.mark.parametrize("S", [9, 16])
+def test_reference_default_width(S) -> None:
+    """S=9 (the reference's default 1 + 8, engine.py:121) and S=16: two query-row tiles per kv
+    head and the row jobs in two rounds; new tokens inside one split, straddling splits, and
+    contexts of only the new tokens."""
+    lens = [S, S + 31, 4100, 2600, 97, 700, 5000, 8192]
+    announce(f"fused attention S={S} lens={lens}")
+    _case(lens, S, 16, 8, 16, seed=20 + S)
+
+
+def test_s9_block_256_and_skipped_slot() -> None:
+    announce("fused attention S=9 block 256, one slot outside the cache")
+    _case([700, 257, 1300, 90], 9, 16, 8, 256, seed=15, bad_slot=True)

@@ -49,7 +49,8 @@ def _order_slack(x: torch.Tensor, w: torch.Tensor) -> np.ndarray:
 
 
 @pytest.mark.parametrize("m,k,n", [(32, 2048, 4096), (32, 2048, 2048), (32, 6144, 2048), (1, 2048, 4096),
-                                   (7, 2048, 160), (64, 2048, 2048), (100, 256, 512), (17, 128, 40)])
+                                   (7, 2048, 160), (64, 2048, 2048), (100, 256, 512), (17, 128, 40),
+                                   (72, 2048, 4096)])
 def test_linear_within_one_ulp(m: int, k: int, n: int) -> None:
     g = torch.Generator(device="cuda").manual_seed(m * 7 + n)
     x, w = _rand(g, m, k), _rand(g, n, k, std=0.02)
@@ -336,3 +337,41 @@ def test_partial_gemm_then_add_rms_norm(k: int) -> None:
     want_h = bf16.to_f32(_bits(wn)).astype(np.float64) * bf16.round_f32((rr * inv).astype(np.float32))
     got_h = bf16.to_f32(_bits(h)).astype(np.float64)
     assert (np.abs(got_h - want_h) <= ATOL + RTOL * np.abs(want_h)).all()
+
+
+@pytest.mark.parametrize("m,k,n,epi", [(72, 2048, 4096, "store"), (80, 2048, 6144, "silu"), (256, 2048, 2048, "partial"),
+                                       (129, 6144, 2048, "partial"), (200, 512, 256, "store"), (72, 2048, 2048, "add")])
+def test_many_rows_equal_64_row_slices(m: int, k: int, n: int, epi: str) -> None:
+    """More than 64 token rows in one call (72 = the reference's default verify width at B=8, up to
+    256 for the decode step): packed rows in, packed rows out, bit-identical to the same rows
+    computed 64 at a time with row-major operands (per-row arithmetic does not depend on the
+    other rows).  Partials land at their rows of the [splits, m, n] array."""
+    g = torch.Generator(device="cuda").manual_seed(7 * m + k + n)
+    x = _rand(g, m, k)
+    w = gemm.pack_weight(_rand(g, 2 * n if epi == "silu" else n, k, std=0.02))
+    xp = gemm.pack_weight(x)
+    announce("many rows", m, k, n, epi)
+    if epi == "partial":
+        splits = gemm.partial_splits(n, k)
+        full = torch.full((splits, m, n), float("nan"), device="cuda")
+        gemm.linear_partial(xp, w, full)
+        for r0 in range(0, m, 64):
+            rows = min(64, m - r0)
+            part = torch.full((splits, rows, n), float("nan"), device="cuda")
+            gemm.linear_partial(x[r0 : r0 + rows].contiguous(), w, part)
+            torch.cuda.synchronize()
+            assert torch.equal(full[:, r0 : r0 + rows].view(torch.int32), part.view(torch.int32)), r0
+        return
+    if epi == "add":
+        r = _rand(g, m, n)
+        full = r.clone()
+        gemm.linear_add_(full, xp.unpack(), w)  # row-major x, one call of all m rows
+        want = torch.cat([gemm.linear_add_(r[r0 : r0 + 64].clone(), x[r0 : r0 + 64], w) for r0 in range(0, m, 64)])
+        torch.cuda.synchronize()
+        assert torch.equal(full.view(torch.int16), want.view(torch.int16))
+        return
+    fn = gemm.linear if epi == "store" else gemm.linear_silu_mul
+    full = fn(xp, w, out=gemm.packed_rows(m, n, "cuda")).unpack()
+    want = torch.cat([fn(x[r0 : r0 + 64].contiguous(), w) for r0 in range(0, m, 64)])
+    torch.cuda.synchronize()
+    assert torch.equal(full.view(torch.int16), want.view(torch.int16))
