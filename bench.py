@@ -325,9 +325,14 @@ def measured_traffic() -> int | None:
 
 
 def pmc_driver(config, model, cache, loop) -> None:
-    """Ten attention launches at the step's shape, then five device copies of COPY_BYTES: the
-    workload of the committed FETCH_SIZE / WRITE_SIZE runs."""
-    time_attention(config, model, cache, loop, iters=10)
+    """Ten attention launches at the step's shape (after 28 untimed ones), then five device copies of
+    COPY_BYTES: the workload of the committed FETCH_SIZE / WRITE_SIZE runs.  Prints the launches'
+    algorithmic bytes (every visible key's K/V once, qkv in, output and new K/V rows out), computed
+    from this run's own context lengths."""
+    attn = time_attention(config, model, cache, loop, iters=10)
+    seq = (loop.seq_len + loop.tokens_per_seq).cpu().tolist()
+    print(json.dumps({"algorithmic_bytes_per_launch": attn["bytes"], "seq_lens": seq, "copy_bytes": COPY_BYTES}),
+          flush=True)
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(5):
@@ -336,12 +341,28 @@ def pmc_driver(config, model, cache, loop) -> None:
     log("pmc driver done")
 
 
+def _cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
 def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict:
-    """The oracle's torch-CPU restatement of one verify step (oracle/decoder.py) on this host."""
+    """The oracle's torch-CPU restatement of one verify step (oracle/decoder.py) on this host, timed
+    as BASELINE.md plans: 3 warm-ups then the median of 10 steps, at all affinity cores; and at
+    one thread (the reference engine pins torch to one, engine.py:207) from a bounded sample --
+    the same step with its layer stack cut to 1 and to 2 layers (3 warm-ups + 10 timed each),
+    whose difference is the cost of one layer, scaled to the model's layer count."""
+    from dataclasses import replace
+    from types import SimpleNamespace
+
     from oracle import decoder as oracle_decoder  # the CPU baseline leg only
 
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     weights = model.weights.unpacked().to("cpu")
     # Compact copy of the pages the batch uses (the GPU pool holds many more).
     used = np.unique(table)
@@ -352,30 +373,42 @@ def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict
     cv = cache.v[:, idx].cpu()
     ctable = remap[table]
     hist = [list(map(int, h)) for h in histories]
-    times, committed = [], []
-    for i in range(args.cpu_warmup + args.cpu_steps):
-        t0 = time.perf_counter()
-        taken = oracle_decoder.verify_step(config, weights, hist, seq_lens, ctable, args.k, args.max_n, ck, cv,
-                                           args.block_size).taken
-        dt = time.perf_counter() - t0
-        if i >= args.cpu_warmup:
-            times.append(dt)
-            committed.append(sum(len(t) for t in taken))
-        log(f"cpu step {i}: {dt:.3f} s")
-    med = float(np.median(times))
-    model_name = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model_name = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+
+    def timed(cfg, w, warm, reps, label):
+        times, committed = [], []
+        for i in range(warm + reps):
+            t0 = time.perf_counter()
+            taken = oracle_decoder.verify_step(cfg, w, hist, seq_lens, ctable, args.k, args.max_n, ck, cv,
+                                               args.block_size).taken
+            dt = time.perf_counter() - t0
+            if i >= warm:
+                times.append(dt)
+                committed.append(sum(len(t) for t in taken))
+        log(f"cpu {label}: median {np.median(times):.3f} s over {reps} (+{warm} warm-up)")
+        return float(np.median(times)), float(np.mean(committed))
+
+    torch.set_num_threads(cores)
+    med, committed = timed(config, weights, args.cpu_warmup, args.cpu_steps, f"{cores} threads")
+    torch.set_num_threads(1)
+    cut = {n: (replace(config, num_layers=n), SimpleNamespace(**{**weights.__dict__, "layers": weights.layers[:n]}))
+           for n in (1, 2)}
+    t1, _ = timed(*cut[1], args.cpu_warmup, args.cpu_steps, "1 thread, 1 layer")
+    t2, _ = timed(*cut[2], args.cpu_warmup, args.cpu_steps, "1 thread, 2 layers")
+    torch.set_num_threads(cores)
+    per_layer = max(t2 - t1, 0.0)
+    one = t1 + (config.num_layers - 1) * per_layer
     return {
-        "value": float(np.mean(committed)) / med, "unit": "accepted tokens/s", "cores": torch.get_num_threads(),
-        "kind": "port", "ms_per_step": med * 1000.0,
-        "sample": f"{args.cpu_steps} timed steps (+{args.cpu_warmup} warm-up) of the same B={args.batch} step, median; "
-                  f"torch {torch.__version__} CPU, {model_name}",
+        "value": committed / med, "unit": "accepted tokens/s", "cores": cores, "kind": "port",
+        "ms_per_step": med * 1000.0,
+        "sample": f"{args.cpu_steps} timed steps (+{args.cpu_warmup} warm-up) of the same B={args.batch} step, median, "
+                  f"{cores} torch threads; torch {torch.__version__} CPU, {_cpu_model_name()}",
+        "one_thread": {
+            "value": committed / one, "unit": "accepted tokens/s", "cores": 1, "ms_per_step": one * 1000.0,
+            "ms_per_layer": per_layer * 1000.0,
+            "sample": f"the step cut to 1 and 2 layers, {args.cpu_steps} timed (+{args.cpu_warmup} warm-up) each at "
+                      f"one thread: {t1 * 1000:.0f} and {t2 * 1000:.0f} ms; one layer = the difference, scaled to "
+                      f"{config.num_layers} layers",
+        },
     }
 
 
@@ -395,9 +428,9 @@ def main() -> int:
     p.add_argument("--max-n", type=int, default=4)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-steps", type=int, default=12)
+    p.add_argument("--cpu-steps", type=int, default=10)
     p.add_argument("--pmc-driver", action="store_true", help="only attention launches + a calibration copy")
-    p.add_argument("--cpu-warmup", type=int, default=1)
+    p.add_argument("--cpu-warmup", type=int, default=3)
     p.add_argument("--prefill-driver", action="store_true", help="only the prefill attention measurement")
     p.add_argument("--configs-driver", action="store_true", help="only the per-kernel configurations 1, 2 and 4")
     args = p.parse_args()

@@ -167,7 +167,9 @@ class NgramProposer:
 
     The history is mirrored on the GPU append-only: ``propose``/``extend`` upload only tokens
     past the mirrored length (a shorter list re-uploads everything).  The index covers positions
-    up to the length at the last ``__init__``/``extend``, as the reference's dict does."""
+    up to the length at the last ``__init__``/``extend``, as the reference's dict does.  One call
+    of ``propose`` costs one host-to-device copy (the new tokens and the two lengths travel in one
+    pinned buffer) and one device-to-host read (the draft and its length together)."""
 
     def __init__(self, tokens: Sequence[int], *, max_n: int = _MAX_N):
         self.max_n = max_n
@@ -175,9 +177,13 @@ class NgramProposer:
         self._buf = torch.zeros(max(64, 2 * len(tokens)), dtype=torch.int32, device=self._device)
         self._mirrored = 0
         self._indexed = len(tokens)
+        self._k = -1
+        self._stage_host = torch.zeros(0, dtype=torch.int32)
+        self._copied: torch.cuda.Event | None = None  # the last upload from the staging buffer
         self._sync(tokens)
 
     def _sync(self, tokens: Sequence[int]) -> None:
+        """Mirror ``tokens`` and stage [len, indexed] for the next launch, in one upload."""
         n = len(tokens)
         if n < self._mirrored:
             self._mirrored = 0
@@ -185,39 +191,56 @@ class NgramProposer:
             grown = torch.zeros(2 * n, dtype=torch.int32, device=self._device)
             grown[: self._mirrored] = self._buf[: self._mirrored]
             self._buf = grown
-        if n > self._mirrored:
-            new = torch.tensor(list(tokens[self._mirrored :]), dtype=torch.int32)
-            self._buf[self._mirrored : n].copy_(new)
-            self._mirrored = n
+        new = n - self._mirrored
+        if self._copied is not None:
+            self._copied.synchronize()  # the staging buffer is rewritten below: its last upload must be done
+        if self._stage_host.numel() < new + 2:
+            self._stage_host = torch.empty(max(2 * (new + 2), 64), dtype=torch.int32).pin_memory()
+            self._stage_dev = torch.empty(self._stage_host.numel(), dtype=torch.int32, device=self._device)
+        host = self._stage_host.numpy()
+        host[0], host[1] = n, self._indexed
+        host[2 : 2 + new] = tokens[self._mirrored :]
+        self._stage_dev[: new + 2].copy_(self._stage_host[: new + 2], non_blocking=True)
+        self._copied = torch.cuda.Event()
+        self._copied.record()
+        if new:
+            self._buf[self._mirrored : n].copy_(self._stage_dev[2 : 2 + new])
+        self._mirrored = n
 
     def extend(self, tokens: Sequence[int], old_length: int) -> None:
         """``tokens`` from ``old_length`` on are new; index them (speculative.py:28-31)."""
-        self._sync(tokens)
         self._indexed = max(self._indexed, len(tokens))
+        self._sync(tokens)
 
     def propose(self, tokens: Sequence[int], k: int) -> list[int]:
         """Up to ``k`` ids following the latest earlier occurrence of the longest matching suffix;
         ``[]`` when nothing matches (speculative.py:33-39)."""
         self._sync(tokens)
         n = len(tokens)
+        k = max(k, 0)
+        if k != self._k:
+            self._out = torch.zeros(k + 1, dtype=torch.int32, device=self._device)  # [len, draft...]
+            self._k = k
         hist = self._buf[:n].view(1, n) if n else self._buf[:1].view(1, 1)
-        length = torch.tensor([n], dtype=torch.int32, device=self._device)
-        index_len = torch.tensor([self._indexed], dtype=torch.int32, device=self._device)
-        draft, draft_len = propose_batch(hist, length, max(k, 0), max_n=self.max_n, index_len=index_len)
-        m = int(draft_len.item())
-        return draft[0, :m].tolist()
+        propose_batch(hist, self._stage_dev[0:1], k, max_n=self.max_n, index_len=self._stage_dev[1:2],
+                      draft=self._out[1:].view(1, k), draft_len=self._out[0:1])
+        out = self._out.tolist()  # the one synchronising read
+        return out[1 : 1 + out[0]]
 
 
 def accept(draft: Sequence[int], predicted: Sequence[int]) -> list[int]:
     """``predicted[j]`` is the model's choice after the previous token and ``draft[:j]``
     (``len(predicted) == len(draft) + 1``).  Returns the matching prefix of ``draft`` plus the model's
-    next choice (speculative.py:42-48)."""
+    next choice (speculative.py:42-48).  One host-to-device copy (draft and predicted ids in one
+    buffer) and one device-to-host read."""
     device = _device()
     k = len(draft)
     _lib.require(len(predicted) >= k + 1, "predicted must hold len(draft) + 1 ids")
-    d = torch.tensor([list(draft) or [0]], dtype=torch.int32).to(device)
-    dl = torch.tensor([k], dtype=torch.int32).to(device)
-    p = torch.tensor([list(predicted[: k + 1])], dtype=torch.int64).to(device)
+    staged = torch.tensor([k, *draft, *predicted[: k + 1]], dtype=torch.int64).pin_memory()
+    dev = staged.to(device, non_blocking=True)
+    d = dev[1 : 1 + k].to(torch.int32).view(1, k) if k else torch.zeros(1, 1, dtype=torch.int32, device=device)
+    dl = dev[0:1].to(torch.int32)
+    p = dev[1 + k : 2 + 2 * k].view(1, k + 1)
     res = accept_batch(d, dl, p)
-    a = int(res.accepted.item())
+    a = int(res.accepted.item())  # the one synchronising read
     return list(draft[:a]) + [int(predicted[a])]
