@@ -22,12 +22,18 @@
 // directly by the main kernel.
 //
 // Per wave, 32 keys at a time (two 16-key MFMA tiles), all in registers:
+//   K and V are read as whole 128-byte cache lines: load instruction q of a
+//     tile gives lane l the 16 bytes [16c, +16) of key 8(q / 2) + l / 8, with
+//     c = 8(q % 2) + l % 8, so 8 consecutive lanes cover one line.  The MFMA
+//     wants lane (r = l % 16, g = l / 16) to hold K[key r][32i + 8g, +8) for
+//     MFMA i; each wave passes its tiles through its own 4.25 KB of LDS to
+//     get there (written in load order, read in fragment order, rows padded
+//     so neither side has bank conflicts).  Measured on loads alone: full
+//     lines with the LDS pass 27.3 us, half-line fragment loads 30.1 us.
 //   S^T tile = K[16 keys x 128] * Q^T           4 v_mfma_f32_16x16x32_bf16 / tile
-//     MFMA i takes dims [32i, 32i + 32): lane (r = l % 16, g = l / 16) loads
-//     K[key r][32i + 8g, +8), its A-operand fragment, so the 4 lanes of a key
-//     read 64 contiguous bytes per instruction (half the cache lines of a
-//     lane-contiguous mapping); Q^T stays in registers in the same mapping.
-//     Lane (r, g) gets the scores of keys 4g..4g+3 of the tile for query row r.
+//     MFMA i takes dims [32i, 32i + 32); Q^T stays in registers in the same
+//     mapping.  Lane (r, g) gets the scores of keys 4g..4g+3 of the tile for
+//     query row r.
 //   online softmax per row in the exp2 domain (scale * log2 e folded in)
 //   V^T fragments by MFMA: V[16 keys x 32 dims] times a 0/1 selector gives
 //     C[key][n] = V[key][n] (or [n + 16]) in the C layout, i.e. lane (n, g) holds
@@ -61,9 +67,13 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 // Context K/V rows: read once per layer and step.
 __device__ __forceinline__ u32x4 ld_kv(const void* p) { return OXR_NT_KV ? ld128_nt(p) : ld128(p); }
 
+// As loaded, register q of tile p holds, in lane l, bytes [16c, +16) of key
+// 16p + 8(q / 2) + l / 8 with c = 8(q % 2) + l % 8 (full lines).  After
+// to_fragments: tile p, MFMA i, lane (r, g) holds key 16p + r, dims
+// [32i + 8g, +8) (K), resp. [32c + 8g, +8) for V's register c.
 struct PairRegs {
-  u32x4 k[2][4];  // tile p: K[key 16p + r][32i + 8g .. +7], i = 0..3
-  u32x4 v[2][4];  // tile p: V[key 16p + r][32c + 8g .. +7], c = 0..3
+  u32x4 k[2][4];
+  u32x4 v[2][4];
 };
 
 // Page numbers of the two 16-key tiles of the pair at t0 (wave-uniform: a
@@ -80,23 +90,48 @@ __device__ __forceinline__ void pair_pages(const int* s_pages, int page0, int t0
   blk1 = blk1 < 0 ? 0 : (blk1 >= num_blocks ? num_blocks - 1 : blk1);
 }
 
-// K and V of the pair at t0 whose tiles lie in pages blk0, blk1.  Keys past
-// L re-read key L - 1: their probabilities are exactly 0 and the cache rows
-// below L hold finite values, so they add nothing.
+// K and V of the pair at t0 whose tiles lie in pages blk0, blk1, in the load
+// layout (whole lines, see PairRegs).  Keys past L re-read key L - 1: their
+// probabilities are exactly 0 and the cache rows below L hold finite values,
+// so they add nothing.
 __device__ __forceinline__ void load_pair(PairRegs& pr, const bf16_t* __restrict__ k_cache,
                                           const bf16_t* __restrict__ v_cache, int64_t blk0, int64_t blk1, int t0,
-                                          int L, int kvh, int KV, int log2_bs, int r, int g) {
+                                          int L, int kvh, int KV, int log2_bs, int lane) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int64_t page = ((p ? blk1 : blk0) << log2_bs) * KV * kD;  // wave-uniform
-    const uint32_t tok = (uint32_t)min(t0 + 16 * p + r, L - 1);
-    const uint32_t off = ((tok & ((1u << log2_bs) - 1)) * (uint32_t)KV + (uint32_t)kvh) * kD;
-    const bf16_t* ks = k_cache + page + off + 8 * g;
-    const bf16_t* vs = v_cache + page + off + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr.k[p][i] = ld_kv(ks + 32 * i);
+    for (int h = 0; h < 2; ++h) {  // keys 8h .. 8h + 7 of the tile
+      const uint32_t tok = (uint32_t)min(t0 + 16 * p + 8 * h + (lane >> 3), L - 1);
+      const uint32_t off = ((tok & ((1u << log2_bs) - 1)) * (uint32_t)KV + (uint32_t)kvh) * kD + 8 * (lane & 7);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) pr.v[p][c] = ld_kv(vs + 32 * c);
+      for (int c3 = 0; c3 < 2; ++c3) {  // bytes [128 c3, +128) of the 256-byte row
+        pr.k[p][2 * h + c3] = ld_kv(k_cache + page + off + 64 * c3);
+        pr.v[p][2 * h + c3] = ld_kv(v_cache + page + off + 64 * c3);
+      }
+    }
+  }
+}
+
+// A pair's K or V tiles from the load layout to the MFMA fragment layout
+// through the wave's LDS exchange buffer, one tile at a time.  The tile is
+// stored as 16 rows of 17 16-byte slots (key, then chunk c = dims [8c, +8)):
+// the 8 lanes of a line write 128 contiguous bytes, and the 16 lanes of a
+// fragment read (16 keys at one chunk) fall in distinct banks.  Both sides
+// address one base register plus immediate offsets.  The wave's LDS
+// operations complete in order, so the reads see the writes and the next
+// tile's writes come after these reads, with no wait or barrier.
+constexpr int kXRow = 17;                 // slots per key row
+constexpr int kXSlots = 16 * kXRow;       // one tile: 4352 bytes
+__device__ __forceinline__ void to_fragments(u32x4 (&t)[2][4], u32x4* xbuf, int lane) {
+  const int wbase = kXRow * (lane >> 3) + (lane & 7);     // key 8h + l / 8, chunk 8c3 + l % 8
+  const int rbase = kXRow * (lane & 15) + (lane >> 4);    // key r, chunk 4i + g
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xbuf[wbase + 8 * kXRow * (q >> 1) + 8 * (q & 1)] = t[p][q];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[p][i] = xbuf[rbase + 4 * i];
   }
 }
 
@@ -157,7 +192,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   // Two row tiles' q fragments (32 registers) would not fit next to two tiles'
   // accumulators and the two pair buffers: with NT = 2 the MFMAs read them from LDS.
   constexpr bool kQinLds = NT == 2;
-  __shared__ float s_o[kWaves][16][kD];   // one row tile's per-wave results at a time
+  __shared__ float s_o[kWaves][16][kD];   // per wave: the K/V exchange buffer, then one row tile's results
   __shared__ u32x4 s_q[kFused || kQinLds ? HPW : 1][kFused || kQinLds ? 16 * NT : 1][kD / 8];
   __shared__ u32x4 s_newk[kFused ? HPW : 1][kFused ? kMaxNew : 1][kD / 8];
   __shared__ u32x4 s_newv[kFused ? HPW : 1][kFused ? kMaxNew : 1][kD / 8];
@@ -269,7 +304,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         f_s8[jr] = ld128(ra.sin_table + row * (kD / 2) + (f_s16 & 7) * 8);
       }
     }
-    load_pair(kv_a, k_cache, v_cache, blk0, blk1, t_first, Lc, kvh, KV, log2_bs, r, g);
+    load_pair(kv_a, k_cache, v_cache, blk0, blk1, t_first, Lc, kvh, KV, log2_bs, lane);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -359,7 +394,13 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     for (int dt = 0; dt < 8; ++dt) o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // The wave's LDS exchange buffer is its own slice of s_o, which the merge
+  // below only uses after this wave's loop.
+  u32x4* const xbuf = reinterpret_cast<u32x4*>(&s_o[wave][0][0]);
+
   auto step = [&](PairRegs& cur, const int t0) {
+    to_fragments(cur.k, xbuf, lane);
+    to_fragments(cur.v, xbuf, lane);
     if constexpr (kFused) {
       if (t0 + 31 >= L - S) {  // wave-uniform: the pair holds new tokens, whose rows come from LDS
 #pragma unroll
@@ -453,15 +494,16 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
       const int ta = t_first + i * stride;
       int64_t blk0, blk1;
       pair_pages(s_pages, page0, min(ta + stride, t_last), L, log2_bs, num_blocks, blk0, blk1);
-      load_pair(kv_b, k_cache, v_cache, blk0, blk1, min(ta + stride, t_last), L, kvh, KV, log2_bs, r, g);
+      load_pair(kv_b, k_cache, v_cache, blk0, blk1, min(ta + stride, t_last), L, kvh, KV, log2_bs, lane);
       __builtin_amdgcn_sched_barrier(0);
       step(kv_a, ta);
       pair_pages(s_pages, page0, min(ta + 2 * stride, t_last), L, log2_bs, num_blocks, blk0, blk1);
-      load_pair(kv_a, k_cache, v_cache, blk0, blk1, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, r, g);
+      load_pair(kv_a, k_cache, v_cache, blk0, blk1, min(ta + 2 * stride, t_last), L, kvh, KV, log2_bs, lane);
       __builtin_amdgcn_sched_barrier(0);
       if (i + 1 < n) step(kv_b, ta + stride);
     }
   }
+  __asm__ __volatile__("" ::: "memory");  // the exchange buffer's last reads stay before the merge's s_o writes
 
   // Merge each head's kStreams waves on chip, one row tile at a time.
 #pragma unroll
