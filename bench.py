@@ -96,13 +96,15 @@ def step_bytes(config, batch, tokens_per_seq, kv_lens_mean) -> dict:
     return {"weights": weights, "kv_read": kv_read, "kv_write": kv_write, "total": weights + kv_read + kv_write}
 
 
-def time_attention(config, model, cache, loop, iters: int = 56) -> dict:
+def time_attention(config, model, cache, loop, context: torch.Tensor, iters: int = 56) -> dict:
     """The dominant kernel: the layer's fused attention launch (q/k norm + RoPE + K/V store + paged
     verify attention, then the split merge) at the step's shape, timed with HIP events on the stream it
-    is launched on.  Launches rotate over the layers' caches, so the K/V comes from HBM as in the step."""
+    is launched on.  Launches rotate over the layers' caches, so the K/V comes from HBM as in the step.
+    `context`: each sequence's committed length before the step (the loaded contexts, so the bench line
+    and the FETCH_SIZE / WRITE_SIZE runs time the same launch)."""
     b, s = loop.batch, loop.tokens_per_seq
     c, w = config, model.weights
-    seq = (loop.seq_len + s).to(torch.int32)
+    seq = (context.to(loop.seq_len.device) + s).to(torch.int32)
     g = torch.Generator(device="cuda").manual_seed(5)
     qkv = (torch.randn(b * s, c.qkv_size, generator=g, device="cuda")).to(torch.bfloat16)
     pos = (seq.to(torch.int64)[:, None] - s + torch.arange(s, device="cuda")[None, :]).reshape(-1)
@@ -329,7 +331,7 @@ def pmc_driver(config, model, cache, loop) -> None:
     COPY_BYTES: the workload of the committed FETCH_SIZE / WRITE_SIZE runs.  Prints the launches'
     algorithmic bytes (every visible key's K/V once, qkv in, output and new K/V rows out), computed
     from this run's own context lengths."""
-    attn = time_attention(config, model, cache, loop, iters=10)
+    attn = time_attention(config, model, cache, loop, loop.seq_len.clone(), iters=10)
     seq = (loop.seq_len + loop.tokens_per_seq).cpu().tolist()
     print(json.dumps({"algorithmic_bytes_per_launch": attn["bytes"], "seq_lens": seq, "copy_bytes": COPY_BYTES}),
           flush=True)
@@ -468,6 +470,7 @@ def main() -> int:
                                    history_capacity=args.history + (args.k + 1) * (args.steps + args.warmup + 8),
                                    table_width=width, device=device)
     loop.load(histories, seq_lens, table)
+    loaded_context = loop.seq_len.clone()
     if args.pmc_driver:
         pmc_driver(config, model, cache, loop)
         return 0
@@ -497,7 +500,7 @@ def main() -> int:
     step_gbs = traffic["total"] / (ms * 1e-3) / 1e9
     log(f"{ms * 1000:.1f} us/step, {committed} tokens committed, step HBM {step_gbs:.0f} GB/s")
 
-    attn = time_attention(config, model, cache, loop)
+    attn = time_attention(config, model, cache, loop, loaded_context)
     attn_gbs = attn["bytes"] / (attn["us"] * 1e-6) / 1e9
     log(f"attention kernel {attn['us']:.2f} us, {attn_gbs:.0f} GB/s")
     decode = time_decode(config, model, cache, loop)
