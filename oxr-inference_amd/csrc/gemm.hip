@@ -86,16 +86,12 @@ struct GemmArgs {
   int64_t part_rows;
 };
 
-#ifndef OXR_NT_PART
-#define OXR_NT_PART 0  // 1: k-split partials stored non-temporally (measurement builds)
-#endif
-#ifndef OXR_NT_W
-#define OXR_NT_W 1  // 0: weights through ordinary loads (measurement builds)
-#endif
 // Weight fragments are streamed once per step, so they are loaded non-temporally: measured on the
 // verify step, 2225 vs 2255 us, the 32-row LM head 103 vs 117 us (6.0 TB/s).  (The context K/V in
-// the attention kernel, also read once, got slower that way: 41.6 vs 36.0 us per launch.)
-__device__ __forceinline__ u32x4 ld_w(const void* p) { return OXR_NT_W ? ld128_nt(p) : ld128(p); }
+// the attention kernel, also read once, got slower that way: 41.6 vs 36.0 us per launch.)  The fp32
+// partials use ordinary stores: non-temporal ones made the step 20 us slower (their reader, the
+// add + RMSNorm that follows, gains from the lines staying cached).
+__device__ __forceinline__ u32x4 ld_w(const void* p) { return ld128_nt(p); }
 
 template <int NT, int NB>
 struct Stage {
@@ -256,8 +252,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(GemmArgs args) {
         const int64_t col0 = n0 + 16 * a + 4 * g;
         float* dst = args.part + ((int64_t)blockIdx.y * args.part_rows + tok) * args.N + col0;
         if (col0 + 3 < args.N) {
-          if (OXR_NT_PART) __builtin_nontemporal_store(acc[a][bt], reinterpret_cast<f32x4*>(dst));
-          else *reinterpret_cast<f32x4*>(dst) = acc[a][bt];
+          *reinterpret_cast<f32x4*>(dst) = acc[a][bt];
         } else {
           for (int j = 0; j < 4; ++j)
             if (col0 + j < args.N) dst[j] = acc[a][bt][j];
@@ -870,29 +865,23 @@ int dispatch(const GemmArgs& a, const LaunchConfig& c, Layout layout, hipStream_
 // at most 8 steps of 128 (o_proj: 1 wave; qkv, gate_up, down_proj: 2).  More
 // waves per workgroup only add requests in flight to an already saturated
 // memory pipeline (4 waves: gate_up 18.1 vs 15.7 us, down_proj 9.9 vs 8.5).
-#ifndef OXR_GEMM_WAVE_STEPS
-#define OXR_GEMM_WAVE_STEPS 8  // most 128-k steps per wave before a GEMM adds waves (measurement builds)
-#endif
-#ifndef OXR_GEMM_NA2_TILES
-#define OXR_GEMM_NA2_TILES 160  // 32-row tiles from which a whole-K GEMM takes two tiles per workgroup
-#endif
-#ifndef OXR_GEMM_TARGET_WGS
-#define OXR_GEMM_TARGET_WGS 256  // workgroups a k-split GEMM aims for (overridable for measurement builds)
-#endif
+constexpr int kWaveSteps = 8;            // most 128-k steps per wave before a GEMM adds waves
+constexpr int kNa2Tiles = 160;           // 32-row tiles from which a whole-K GEMM takes two tiles per workgroup
+constexpr int kTargetWorkgroups = 256;   // workgroups a k-split GEMM aims for
 LaunchConfig choose_config(int64_t n_rows, int64_t K, bool allow_k_splits) {
   LaunchConfig c{1, 1, 1};
   if (allow_k_splits) {
     c.na = 2;
     const int64_t tiles = (n_rows + 31) / 32;
-    while (tiles * c.k_splits < OXR_GEMM_TARGET_WGS && K % (2 * c.k_splits * kKStep) == 0 && c.k_splits < 16)
+    while (tiles * c.k_splits < kTargetWorkgroups && K % (2 * c.k_splits * kKStep) == 0 && c.k_splits < 16)
       c.k_splits *= 2;
   } else {
-    c.na = (n_rows + 31) / 32 >= OXR_GEMM_NA2_TILES ? 2 : 1;
+    c.na = (n_rows + 31) / 32 >= kNa2Tiles ? 2 : 1;
   }
   const int64_t k_slice = K / c.k_splits;
   // At most 4 waves: an 8-wave workgroup has 256 registers per wave, and its 3- and 4-tile token
   // forms spill (up to 1.1 KiB per lane).
-  while (k_slice / c.waves > OXR_GEMM_WAVE_STEPS * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 4)
+  while (k_slice / c.waves > kWaveSteps * kKStep && k_slice % (2 * c.waves * kKStep) == 0 && c.waves < 4)
     c.waves *= 2;
   return c;
 }

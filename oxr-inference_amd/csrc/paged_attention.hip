@@ -58,14 +58,10 @@ constexpr uint32_t kBf16One = 0x3f80u;
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-#ifndef OXR_NT_PART
-#define OXR_NT_PART 0  // 1: split partials stored non-temporally (measurement builds)
-#endif
-#ifndef OXR_NT_KV
-#define OXR_NT_KV 0  // 1: context K/V through non-temporal loads (measurement builds)
-#endif
-// Context K/V rows: read once per layer and step.
-__device__ __forceinline__ u32x4 ld_kv(const void* p) { return OXR_NT_KV ? ld128_nt(p) : ld128(p); }
+// Context K/V rows are read once per layer and step, but through ordinary loads: non-temporal ones
+// made the launch slower (41.6 vs 36.0 us).  The split partials use ordinary stores too: non-temporal
+// ones made the step 11 us slower (the merge kernel gains from the lines staying cached).
+__device__ __forceinline__ u32x4 ld_kv(const void* p) { return ld128(p); }
 
 // As loaded, register q of tile p holds, in lane l, bytes [16c, +16) of key
 // 16p + 8(q / 2) + l / 8 with c = 8(q % 2) + l % 8 (full lines).  After
@@ -544,8 +540,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
       } else {
         f32x4* const po = reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kPartRows + rr) * kD + d0);
-        if (OXR_NT_PART) __builtin_nontemporal_store(acc, po);
-        else *po = acc;
+        *po = acc;
         if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + ((unit0 + split) * kPartRows + rr) * 2) = f32x2{mmax, l};
       }
     }
@@ -607,10 +602,7 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
 // workgroup per CU over the whole batch, but at least kMinSplitKeys keys of
 // the longest context per split.  (At B = 1, 256 workgroups would leave 64
 // keys each: the launch is then fixed cost, and the merge walks 64 partials.)
-#ifndef OXR_ATTN_MIN_SPLIT_KEYS
-#define OXR_ATTN_MIN_SPLIT_KEYS 256  // (overridable for measurement builds)
-#endif
-constexpr int kMinSplitKeys = OXR_ATTN_MIN_SPLIT_KEYS;
+constexpr int kMinSplitKeys = 256;
 int splits_for(int32_t batch, int32_t num_kv_heads, int hpw, int32_t max_seq_len) {
   const int64_t units = (int64_t)batch * (num_kv_heads / hpw);
   int64_t splits = (256 + units - 1) / units;
@@ -618,10 +610,6 @@ int splits_for(int32_t batch, int32_t num_kv_heads, int hpw, int32_t max_seq_len
   splits = splits < by_keys ? splits : by_keys;
   return (int)(splits < 1 ? 1 : (splits > 64 ? 64 : splits));
 }
-
-#ifndef OXR_ATTN_HPW
-#define OXR_ATTN_HPW 0  // 0: choose; 1 or 2: force (for measurement builds)
-#endif
 
 // kv heads per workgroup: two heads read 512-byte slices of each token row
 // together (the heads of a row are adjacent) -- measured 1 us faster per
@@ -632,7 +620,6 @@ int splits_for(int32_t batch, int32_t num_kv_heads, int hpw, int32_t max_seq_len
 int pick_hpw(int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads) {
   const int jobs_per_head = tokens_per_seq * (num_heads / num_kv_heads + 2);
   for (int hpw : {2, 1}) {
-    if (OXR_ATTN_HPW != 0 && hpw != OXR_ATTN_HPW) continue;
     if (num_kv_heads % hpw != 0 || hpw * jobs_per_head > kJobSlots) continue;
     return hpw;
   }

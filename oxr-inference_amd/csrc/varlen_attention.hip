@@ -37,10 +37,6 @@
 // groups alternating softmax and MFMA phases on each SIMD).
 #include "common.h"
 
-#ifndef OXR_VARLEN_PINGPONG
-#define OXR_VARLEN_PINGPONG 1  // 0: the 4-wave kernel (for measurement builds)
-#endif
-
 namespace oxr {
 namespace {
 
@@ -563,7 +559,7 @@ extern "C" int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const 
                 OXR_ERR_UNSUPPORTED);
   // Bidirectional prefill runs the ping-pong kernel; the causal form of that kernel needs more
   // registers than two waves per SIMD have (it spills), so causal prefill runs the 4-wave kernel.
-  const bool pingpong = OXR_VARLEN_PINGPONG != 0 && !causal;
+  const bool pingpong = !causal;
   const int rows_per_head = (pingpong ? kPRows : kVRows) / G;
   const int num_qtiles = (max_len + rows_per_head - 1) / rows_per_head;
   OXR_RETURN_IF((int64_t)num_qtiles * num_kv_heads * num_seqs > INT32_MAX, OXR_ERR_UNSUPPORTED);
