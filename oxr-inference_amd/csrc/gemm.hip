@@ -568,10 +568,53 @@ __device__ __forceinline__ f32x16 mfma_32x32x16(const u32x4& a, const u32x4& b, 
                                                  0, 0);
 }
 
+// The TT token-row fragments of one k16 step from LDS: 16 bytes per lane at byte address a + 4096 tt,
+// all requested before one wait, in one asm block.  As inline asm the reads are invisible to the
+// compiler's tracking of the token-row loads into LDS; that tracking cannot tell across the loop's back
+// edge which load wrote a buffer, and would otherwise wait for every load in flight once per pass.
+// The counted waits and barriers around the reads already order them after those loads.
+template <int TT>
+__device__ __forceinline__ void lds_fragments(u32x4 (&x)[TT], uint32_t a);
+template <>
+__device__ __forceinline__ void lds_fragments<2>(u32x4 (&x)[2], uint32_t a) {
+  asm volatile(
+      "ds_read_b128 %0, %2\n\t"
+      "ds_read_b128 %1, %2 offset:4096\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1])
+      : "v"(a));
+}
+template <>
+__device__ __forceinline__ void lds_fragments<4>(u32x4 (&x)[4], uint32_t a) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %4 offset:4096\n\t"
+      "ds_read_b128 %2, %4 offset:8192\n\t"
+      "ds_read_b128 %3, %4 offset:12288\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
+      : "v"(a));
+}
+template <>
+__device__ __forceinline__ void lds_fragments<8>(u32x4 (&x)[8], uint32_t a) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:4096\n\t"
+      "ds_read_b128 %2, %8 offset:8192\n\t"
+      "ds_read_b128 %3, %8 offset:12288\n\t"
+      "ds_read_b128 %4, %8 offset:16384\n\t"
+      "ds_read_b128 %5, %8 offset:20480\n\t"
+      "ds_read_b128 %6, %8 offset:24576\n\t"
+      "ds_read_b128 %7, %8 offset:28672\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), "=&v"(x[7])
+      : "v"(a));
+}
+
 // TT: 32-token tiles computed (2, 4 or 8; rows past M are padding whose results nobody reads).
 template <int K, int TT>
 __global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf16_t* __restrict__ xp, int M,
-                                                                      const bf16_t* __restrict__ w, int64_t N,
+                                                                      const bf16_t* w, int64_t N,
                                                                       bf16_t* __restrict__ logits, int64_t ldl,
                                                                       uint64_t* __restrict__ best_out) {
   constexpr int kChunks = K / kWideChunk;
@@ -661,15 +704,15 @@ __global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf1
         // This stage's weight chunk (loaded during stage s - 2) is in: the loads issued after it are stage
         // s - 1's and this stage's token rows and stage s - 1's weights.
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kXBlocksPerWave + 4));
-        const bf16_t* xb = bufs[d & 3];
+        // Lane (n, h)'s fragment of token tile tt, k16 step kk: X[32 tt + n][64 c + 16 kk + 8h, +8) at element
+        // (4 tt + 2 (n / 16)) * 512 + (kk / 2) * 512 + (16 (2 (kk % 2) + h) + r) * 8 of the buffer.
+        const uint32_t xb = (uint32_t)(uintptr_t)bufs[d & 3] + 2048 * (n >> 4) + 16 * (16 * h + r);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const int off = (kk >> 1) * 512 + (16 * (2 * (kk & 1) + h) + r) * 8;
+          u32x4 xf[TT];
+          lds_fragments<TT>(xf, xb + 1024 * (kk >> 1) + 512 * (kk & 1));
 #pragma unroll
-          for (int tt = 0; tt < TT; ++tt) {
-            const u32x4 bf = *reinterpret_cast<const u32x4*>(xb + (2 * (2 * tt + (n >> 4))) * 512 + off);
-            acc[tt] = mfma_32x32x16(ring[d % kWideDepth][kk], bf, acc[tt]);
-          }
+          for (int tt = 0; tt < TT; ++tt) acc[tt] = mfma_32x32x16(ring[d % kWideDepth][kk], xf[tt], acc[tt]);
         }
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) ring[d % kWideDepth][kk] = wfrag(s + kWideDepth, kk);
