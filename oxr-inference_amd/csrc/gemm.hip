@@ -639,18 +639,20 @@ __global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf1
   for (int i = tid; i < kWideWaves * kWideMaxRows; i += 64 * kWideWaves) (&wave_best[0][0])[i] = 0;
 
   // Weight fragment of stage s (group s / kChunks, chunk s % kChunks), k16 step kk: lane (n, h) holds
-  // W[32 vt + n][64 c + 16 kk + 8h, +8).  Past this workgroup's range (or a vocab tile it does not own in
-  // its last group) a lane re-reads a valid row whose products nobody uses.
+  // W[32 vt + n][64 c + 16 kk + 8h, +8).  A wave without a vocab tile in a group (the last group of a
+  // range that is not a multiple of kWideWaves, or past the last stage) still issues the load, so every
+  // wave's counted waits hold, but reads the same offset in the first token-row tile (cached, in range:
+  // the offset is below 16 K) and computes nothing with it.
   auto wfrag = [&](int64_t s, int kk) {
     s = s < stages ? s : stages - 1;
     const int64_t gi = s / kChunks;
     const int c = (int)(s - gi * kChunks);
-    int64_t vt = lo + gi * kWideWaves + wave;
-    vt = vt < hi ? vt : hi - 1;
+    const int64_t vt = lo + gi * kWideWaves + wave;
     int64_t t = 2 * vt + (n >> 4);
     t = t < w_last ? t : w_last;
     const int i = 2 * (c & 1) + (kk >> 1), g = 2 * (kk & 1) + h;
-    return ld_w(w + t * (K * 16) + (c >> 1) * (16 * kKStep) + i * 512 + (16 * g + r) * 8);
+    const int64_t inner = (c >> 1) * (16 * kKStep) + i * 512 + (16 * g + r) * 8;
+    return ld_w((vt < hi ? w + t * (K * 16) : xp) + inner);  // vt < hi is wave-uniform
   };
   // Token rows of chunk c straight into an LDS buffer (global_load_lds, 16 bytes per lane: lane i of an
   // instruction writes bytes [16i, 16i + 16) of a 1 KiB block): 32 blocks (block j: token row tile j / 2,
@@ -693,6 +695,9 @@ __global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf1
   static_assert(kChunks % kUnroll == 0 && kUnroll % kWideDepth == 0 && kUnroll % 4 == 0,
                 "ring slots and buffers must be static");
   for (int64_t gi = 0; gi < groups; ++gi) {
+    // Waves without a vocab tile in this group skip the products (wave-uniform); their loads and
+    // barriers are the same as everyone's.
+    const bool active = lo + gi * kWideWaves + wave < hi;
     for (int c0 = 0; c0 < kChunks; c0 += kUnroll) {
 #pragma unroll
       for (int d = 0; d < kUnroll; ++d) {
@@ -707,12 +712,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void lm_head_wide_kernel(const bf1
         // Lane (n, h)'s fragment of token tile tt, k16 step kk: X[32 tt + n][64 c + 16 kk + 8h, +8) at element
         // (4 tt + 2 (n / 16)) * 512 + (kk / 2) * 512 + (16 (2 (kk % 2) + h) + r) * 8 of the buffer.
         const uint32_t xb = (uint32_t)(uintptr_t)bufs[d & 3] + 2048 * (n >> 4) + 16 * (16 * h + r);
+        if (active) {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          u32x4 xf[TT];
-          lds_fragments<TT>(xf, xb + 1024 * (kk >> 1) + 512 * (kk & 1));
+          for (int kk = 0; kk < 4; ++kk) {
+            u32x4 xf[TT];
+            lds_fragments<TT>(xf, xb + 1024 * (kk >> 1) + 512 * (kk & 1));
 #pragma unroll
-          for (int tt = 0; tt < TT; ++tt) acc[tt] = mfma_32x32x16(ring[d % kWideDepth][kk], xf[tt], acc[tt]);
+            for (int tt = 0; tt < TT; ++tt) acc[tt] = mfma_32x32x16(ring[d % kWideDepth][kk], xf[tt], acc[tt]);
+          }
         }
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) ring[d % kWideDepth][kk] = wfrag(s + kWideDepth, kk);
