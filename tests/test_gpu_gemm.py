@@ -277,6 +277,29 @@ def test_lm_head_wide_rows_packed(rows) -> None:
     assert np.array_equal(pred, pred_only.cpu().numpy())
 
 
+@pytest.mark.parametrize("rows", [32, 8, 1])
+def test_lm_head_step_rows_exact(rows) -> None:
+    """The verify step's own LM head (persistent kernel, up to 32 token rows, packed weight) at the
+    full vocab: logits within tolerance of the exact product, ids equal to the oracle's argmax of the
+    exact logits where the margin is clear, and always the first argmax of the kernel's bf16 logits."""
+    g = torch.Generator(device="cuda").manual_seed(70 + rows)
+    hidden, weight = _rand(g, rows, 2048), _rand(g, 151_936, 2048, std=0.02)
+    packed = gemm.pack_weight(weight)
+    announce("lm head step rows", rows)
+    pred, logits = lm_head.lm_head_argmax(hidden, packed, return_logits=True)
+    torch.cuda.synchronize()
+    exact = _exact(hidden, weight)
+    got = bf16.to_f32(_bits(logits)).astype(np.float64)
+    assert (np.abs(got - exact) <= ATOL + RTOL * np.abs(exact)).all()
+    ref_ids = oracle_lm_head.argmax(bf16.from_f32(exact.astype(np.float32)))
+    sure = oracle_lm_head.top2_margin(exact) > ATOL
+    pred = pred.cpu().numpy()
+    if rows >= 8:
+        assert sure.mean() > 0.8
+    assert np.array_equal(pred[sure], ref_ids[sure])
+    assert np.array_equal(pred, oracle_lm_head.argmax(_bits(logits)))
+
+
 def test_lm_head_wide_ties_take_lowest_index() -> None:
     g = torch.Generator(device="cuda").manual_seed(42)
     vocab, k = 20_000, 1024
