@@ -75,7 +75,8 @@ int oxr_ngram_propose(const int32_t* history, int64_t history_stride, const int3
  * Drafts are further capped by the room engine.py:683-684 leaves:
  * k_b <= max_tokens[b] - L - 1 (when max_tokens is non-null) and
  * k_b <= max_positions - seq_len[b] - 1 (when max_positions > 0).
- * tokens_per_seq (S) must be >= k + 1.  ids/positions/slots are int64 [B*S].
+ * tokens_per_seq (S) must be >= k + 1 and at most 256 (OXR_ERR_UNSUPPORTED beyond).
+ * ids/positions/slots are int64 [B*S].
  */
 int oxr_propose_verify_inputs(const int32_t* history, int64_t history_stride, const int32_t* history_len,
                               int32_t batch, int32_t max_n, int32_t k, const int32_t* k_limit,

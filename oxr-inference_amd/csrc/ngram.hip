@@ -9,12 +9,15 @@
 // maximises the key (m(p), p).
 //
 // One 256-thread workgroup per sequence scans candidates from the end of the
-// history backwards in tiles of 256 (one candidate per lane).  Each tile's
-// window of history (256 + max_n tokens) is staged in LDS with coalesced
-// loads, every lane computes m(p) from LDS, and per wave a ballot per n
-// (longest first) plus find-last-set picks the latest p; the four waves then
-// combine through LDS.  The scan stops as soon as a full-length match is
-// found: nothing earlier can beat it.
+// history backwards in chunks of up to 4096.  A chunk's window of history
+// (4096 + max_n tokens) is staged in LDS in one round of coalesced loads, so a
+// typical history costs one memory latency.  Each wave then walks its own
+// 64-candidate tiles of the chunk (tile w, w + 4, ... from the top, one
+// candidate per lane): every lane computes m(p) from LDS, and a ballot per n
+// (longest first, only lengths that beat the wave's best so far) plus
+// find-last-set picks the latest p.  The four waves combine through LDS once
+// per chunk.  A wave stops at a full-length match, and so does the scan:
+// nothing earlier can beat it.
 #include "common.h"
 
 namespace oxr {
@@ -23,6 +26,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxN = 8;
 constexpr int kMaxDraft = 64;
+constexpr int kChunk = 4096;  // candidates per LDS-staged chunk (16 KiB)
+constexpr int kStage = (kChunk + kMaxN + kThreads - 1) / kThreads;  // history tokens each thread stages
 
 // Where the verify inputs go when drafting also assembles them (engine.py:700-710).
 struct VerifyInputs {
@@ -46,7 +51,7 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
                                                                  int k, const int32_t* __restrict__ k_limit,
                                                                  int32_t* __restrict__ draft,
                                                                  int32_t* __restrict__ draft_len, VerifyInputs vi) {
-  __shared__ int32_t window[kThreads + kMaxN];
+  __shared__ int32_t window[kChunk + kMaxN];
   __shared__ int32_t wave_n[kThreads / kWave];
   __shared__ int32_t wave_p[kThreads / kWave];
 
@@ -66,37 +71,66 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
 #pragma unroll
   for (int i = 0; i < kMaxN; ++i) suffix[i] = (i < nmax) ? h[L - 1 - i] : 0;
 
+  // The verify row's positions and slots do not depend on the drafts: thread j < S
+  // looks up its slot now, while the history loads are in flight.
+  int base_len = 0;
+  int64_t my_slot = -1;
+  if constexpr (kAssemble) {
+    base_len = vi.seq_len[b];
+    if (tid < vi.tokens_per_seq) {
+      const int64_t pos = (int64_t)base_len + tid;
+      const int64_t blk = pos / vi.block_size;
+      if (pos >= 0 && blk < vi.table_stride) {
+        const int32_t page = vi.block_table[(int64_t)b * vi.table_stride + blk];
+        if (page >= 0) my_slot = (int64_t)page * vi.block_size + pos % vi.block_size;
+      }
+    }
+  }
+
   int best_n = 0, best_p = -1;
-  for (int top = last; top >= 1 && nmax > 0; top -= kThreads) {
-    const int base = top - (kThreads - 1);  // candidate of thread 0 (may be < 1)
-    // Stage h[base - kMaxN, top) into LDS.
-    for (int i = tid; i < kThreads + kMaxN; i += kThreads) {
+  for (int top = last; top >= 1 && nmax > 0; top -= kChunk) {
+    const int base = top - (kChunk - 1);  // candidate at window index kMaxN (may be < 1)
+    // Stage h[base - kMaxN, top) into LDS: every load is issued before any store.
+    int32_t staged[kStage];
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int i = tid + u * kThreads;
       const int pos = base - kMaxN + i;
-      window[i] = (pos >= 0 && pos < L) ? h[pos] : 0;
+      staged[u] = (i < kChunk + kMaxN && pos >= 0 && pos < L) ? h[pos] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int i = tid + u * kThreads;
+      if (i < kChunk + kMaxN) window[i] = staged[u];
     }
     __syncthreads();
 
-    const int p = base + tid;
-    int m = 0;
-    if (p >= 1) {
-      const int cap = min(nmax, p);
-#pragma unroll
-      for (int i = 0; i < kMaxN; ++i) {
-        if (i >= cap || m != i) break;
-        // h[p - 1 - i] sits at window index (p - 1 - i) - (base - kMaxN).
-        if (window[tid + kMaxN - 1 - i] == suffix[i]) m = i + 1;
-      }
-    }
-
-    // Per wave: longest n first, latest lane (largest p) via find-last-set.
+    // This wave's tiles, from the top down.  Within a wave a lower tile only wins
+    // with a strictly longer match, so the ballots test only such lengths.
     int wn = 0, wp = -1;
-    for (int n = nmax; n >= 1; --n) {
-      const unsigned long long mask = __ballot(m >= n);
-      if (mask) {
-        wn = n;
-        wp = base + wave * kWave + (63 - __clzll(mask));
-        break;
+    for (int t = wave; t < kChunk / kWave; t += kThreads / kWave) {
+      const int p0 = top - kWave * t - (kWave - 1);  // candidate of lane 0
+      if (p0 + kWave - 1 < 1) break;                // wave-uniform: below candidate 1
+      const int p = p0 + lane;
+      int m = 0;
+      if (p >= 1) {
+        const int cap = min(nmax, p);
+#pragma unroll
+        for (int i = 0; i < kMaxN; ++i) {
+          if (i >= cap || m != i) break;
+          // h[p - 1 - i] sits at window index (p - 1 - i) - (base - kMaxN).
+          if (window[p - 1 - i - base + kMaxN] == suffix[i]) m = i + 1;
+        }
       }
+      for (int n = nmax; n > wn; --n) {
+        const unsigned long long mask = __ballot(m >= n);
+        if (mask) {
+          wn = n;
+          wp = p0 + (63 - __clzll(mask));
+          break;
+        }
+      }
+      if (wn == nmax) break;  // nothing lower in this wave beats a full-length match
     }
     if (lane == 0) {
       wave_n[wave] = wn;
@@ -111,13 +145,13 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
         tp = wave_p[w];
       }
     }
-    // Later tiles already hold the latest p for any length they matched, so an
-    // earlier tile only wins with a strictly longer match.
+    // Later chunks already hold the latest p for any length they matched, so an
+    // earlier chunk only wins with a strictly longer match.
     if (tn > best_n) {
       best_n = tn;
       best_p = tp;
     }
-    __syncthreads();  // window / wave_* are rewritten by the next tile
+    __syncthreads();  // window / wave_* are rewritten by the next chunk
     if (best_n == nmax) break;
   }
 
@@ -140,23 +174,16 @@ __global__ __launch_bounds__(kThreads) void ngram_propose_kernel(const int32_t* 
     // (engine.py:700-710, language.py:320-322).  A position past the block
     // table, or on a negative (unallocated) table entry, gets slot -1, which
     // the KV write skips.
-    const int S = vi.tokens_per_seq;
-    const int base_len = vi.seq_len[b];
-    for (int j = tid; j < S; j += kThreads) {
+    const int S = vi.tokens_per_seq;  // <= kThreads (checked on the host)
+    if (tid < S) {
+      const int j = tid;
       int64_t id = 0;
       if (j == 0) id = (L > 0) ? h[L - 1] : 0;
       else if (j - 1 < len) id = h[best_p + j - 1];
-      const int64_t pos = (int64_t)base_len + j;
-      const int64_t blk = pos / vi.block_size;
-      int64_t slot = -1;
-      if (pos >= 0 && blk < vi.table_stride) {
-        const int32_t page = vi.block_table[(int64_t)b * vi.table_stride + blk];
-        if (page >= 0) slot = (int64_t)page * vi.block_size + pos % vi.block_size;
-      }
       const int64_t row = (int64_t)b * S + j;
       vi.ids[row] = id;
-      vi.positions[row] = pos;
-      vi.slots[row] = slot;
+      vi.positions[row] = (int64_t)base_len + j;
+      vi.slots[row] = my_slot;
     }
     if (tid == 0) vi.attn_seq_lens[b] = base_len + S;
   }
@@ -189,6 +216,7 @@ extern "C" int oxr_propose_verify_inputs(const int32_t* history, int64_t history
   OXR_RETURN_IF(batch < 0 || k < 0 || history_stride < 0 || table_stride < 0 || block_size <= 0,
                 OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(tokens_per_seq < k + 1, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(tokens_per_seq > kThreads, OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(max_n < 1 || max_n > kMaxN || k > kMaxDraft, OXR_ERR_UNSUPPORTED);
   if (batch == 0) return OXR_OK;
   OXR_RETURN_IF(!history || !history_len || !draft_len || (k > 0 && !draft) || !seq_len || !block_table || !ids ||
