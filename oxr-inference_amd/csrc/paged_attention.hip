@@ -507,7 +507,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const float l_tot = xor32_sum(xor16_sum(l_run[t]));
     if (t > 0) __syncthreads();  // the previous tile's merge has read s_o, s_m, s_l
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[t][dt];
+    for (int dt = 0; dt < 8; ++dt)  // real rows only: the merge below reads rows < R
+      if (16 * t + r < R) *reinterpret_cast<f32x4*>(&s_o[wave][r][dt * 16 + 4 * g]) = o[t][dt];
     if (g == 0) {
       s_m[wave][r] = m_run[t] == -INFINITY ? -INFINITY : mc_run[t];
       s_l[wave][r] = l_tot;
