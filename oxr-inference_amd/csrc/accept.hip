@@ -27,28 +27,68 @@ __global__ __launch_bounds__(64) void accept_kernel(const int32_t* __restrict__ 
                                                     int32_t* __restrict__ finished) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
-  if (finished && finished[b] != 0) {  // a finished sequence takes no tokens
+  // Every input of this sequence is requested before any is used (one memory round trip):
+  // the first kPre drafts and predictions, the lengths and the limits.
+  constexpr int kPre = 8;
+  // Loads are unconditional (a missing optional array reads draft_len[b] instead and the value is
+  // discarded), so the compiler issues them together rather than one per branch.
+  const int32_t* const any = draft_len + b;
+  const int32_t fin_raw = *(finished ? finished + b : any);
+  const int n_raw = draft_len[b];
+  const int32_t* d = k > 0 ? draft + (int64_t)b * k : any;
+  const int64_t* pred = predicted + (int64_t)b * S;
+  int32_t dv[kPre];
+  int64_t pv[kPre + 1];
+#pragma unroll
+  for (int j = 0; j < kPre; ++j) dv[j] = d[k > 0 ? min(j, k - 1) : 0];
+#pragma unroll
+  for (int j = 0; j <= kPre; ++j) pv[j] = pred[min(j, S - 1)];
+  const int32_t len0_raw = *(history ? history_len + b : any);
+  const int32_t cap_raw = *(max_tokens ? max_tokens + b : any);
+  const int32_t sl_raw = *(seq_len ? seq_len + b : any);
+  // Keep every load above ahead of the first use (the compiler would otherwise sink them past the
+  // finished-sequence branch, one round trip each).
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::"v"(fin_raw), "v"(n_raw), "v"(len0_raw), "v"(cap_raw), "v"(sl_raw));
+#pragma unroll
+  for (int j = 0; j < kPre; ++j) asm volatile("" ::"v"(dv[j]));
+#pragma unroll
+  for (int j = 0; j <= kPre; ++j) asm volatile("" ::"v"(pv[j]));
+  const int32_t fin = finished ? fin_raw : 0;
+  const int32_t len0 = history ? len0_raw : 0;
+  const int32_t cap = max_tokens ? cap_raw : 0;
+  const int32_t sl = seq_len ? sl_raw : 0;
+
+  if (fin != 0) {  // a finished sequence takes no tokens
     accepted[b] = 0;
     if (num_committed) num_committed[b] = 0;
     if (committed)
       for (int j = 0; j <= k; ++j) committed[(int64_t)b * (k + 1) + j] = -1;
     return;
   }
-  const int n = min(max(draft_len[b], 0), min(k, S - 1));
-  const int32_t* d = draft + (int64_t)b * k;
-  const int64_t* pred = predicted + (int64_t)b * S;
+  const int n = min(max(n_raw, 0), min(k, S - 1));
+  auto pred_at = [&](int j) -> int64_t {
+    int64_t v = pred[j];  // past the preloaded ones
+#pragma unroll
+    for (int i = 0; i <= kPre; ++i)
+      if (j == i) v = pv[i];
+    return v;
+  };
   int a = 0;
-  while (a < n && (int64_t)d[a] == pred[a]) ++a;
+#pragma unroll
+  for (int j = 0; j < kPre; ++j)
+    if (a == j && a < n && (int64_t)dv[j] == pv[j]) ++a;
+  while (a >= kPre && a < n && (int64_t)d[a] == pred[a]) ++a;  // drafts beyond the preloaded ones
   accepted[b] = a;
   if (num_committed) num_committed[b] = a + 1;
   if (committed)
-    for (int j = 0; j <= k; ++j) committed[(int64_t)b * (k + 1) + j] = (j <= a) ? (int32_t)pred[j] : -1;
-  if (seq_len) seq_len[b] += a + 1;
+    for (int j = 0; j <= k; ++j) committed[(int64_t)b * (k + 1) + j] = (j <= a) ? (int32_t)pred_at(j) : -1;
+  if (seq_len) seq_len[b] = sl + a + 1;
   if (history) {
-    int len = history_len[b];
+    int len = len0;
     int reason = 0;
     for (int j = 0; j <= a; ++j) {
-      const int32_t t = (int32_t)pred[j];
+      const int32_t t = (int32_t)pred_at(j);
       if (t == eos_id) {
         reason = 1;
         break;
@@ -59,7 +99,7 @@ __global__ __launch_bounds__(64) void accept_kernel(const int32_t* __restrict__ 
       }
       history[(int64_t)b * history_stride + len] = t;
       ++len;
-      if (max_tokens && len >= max_tokens[b]) {
+      if (max_tokens && len >= cap) {
         reason = 2;
         break;
       }

@@ -563,6 +563,12 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
   // One thread per 4 output dims of a row (blockDim = rows * 32).
   const int rr = threadIdx.x / (kD / 4), d0 = (threadIdx.x % (kD / 4)) * 4;
   const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
+  // The context length is only needed at the end, but it is requested first so that its
+  // latency overlaps the partials' instead of following it.  (As inline asm: the compiler
+  // would sink an ordinary load of it to its use.  Being older than every load below, it
+  // leaves the compiler's own counted waits exact; the explicit wait before its use covers it.)
+  int seq_len_b;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(seq_len_b) : "v"(seq_lens + b) : "memory");
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < splits; c0 += kChunk) {
@@ -576,6 +582,7 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
       ml[j] = *reinterpret_cast<const f32x2*>(part_ml + (u * kPartRows + rr) * 2);
       v[j] = *reinterpret_cast<const f32x4*>(part_o + (u * kPartRows + rr) * kD + d0);
     }
+    __builtin_amdgcn_sched_barrier(0);  // all of the chunk's loads go out before the first use
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
       const float mj = c0 + j < splits ? ml[j][0] : -INFINITY;
@@ -589,7 +596,8 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
   }
   // Sequences whose context fitted one split were stored by the main kernel
   // (checked only now, so the partials above were requested without waiting).
-  const int L = min(seq_lens[b], max_seq_len);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the length load has landed
+  const int L = min(seq_len_b, max_seq_len);
   const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
   if (L <= span) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
