@@ -67,13 +67,6 @@ __global__ __launch_bounds__(64) void accept_kernel(const int32_t* __restrict__ 
     return;
   }
   const int n = min(max(n_raw, 0), min(k, S - 1));
-  auto pred_at = [&](int j) -> int64_t {
-    int64_t v = pred[j];  // past the preloaded ones
-#pragma unroll
-    for (int i = 0; i <= kPre; ++i)
-      if (j == i) v = pv[i];
-    return v;
-  };
   int a = 0;
 #pragma unroll
   for (int j = 0; j < kPre; ++j)
@@ -81,29 +74,42 @@ __global__ __launch_bounds__(64) void accept_kernel(const int32_t* __restrict__ 
   while (a >= kPre && a < n && (int64_t)d[a] == pred[a]) ++a;  // drafts beyond the preloaded ones
   accepted[b] = a;
   if (num_committed) num_committed[b] = a + 1;
-  if (committed)
-    for (int j = 0; j <= k; ++j) committed[(int64_t)b * (k + 1) + j] = (j <= a) ? (int32_t)pred_at(j) : -1;
+  // Token j of the committed run is pv[j] for j <= kPre (static indices only: a dynamically
+  // indexed register array would be placed in scratch memory), else loaded again.
+  if (committed) {
+    int32_t* const row = committed + (int64_t)b * (k + 1);
+#pragma unroll
+    for (int j = 0; j <= kPre; ++j)
+      if (j <= k) row[j] = (j <= a) ? (int32_t)pv[j] : -1;
+    for (int j = kPre + 1; j <= k; ++j) row[j] = (j <= a) ? (int32_t)pred[j] : -1;
+  }
   if (seq_len) seq_len[b] = sl + a + 1;
   if (history) {
     int len = len0;
     int reason = 0;
-    for (int j = 0; j <= a; ++j) {
-      const int32_t t = (int32_t)pred_at(j);
+    bool stop = false;
+    auto take = [&](int32_t t) {  // history.append with the engine's stop rules
       if (t == eos_id) {
         reason = 1;
-        break;
+        stop = true;
+        return;
       }
       if (len >= history_stride) {  // buffer full: stop as a length finish
         reason = 2;
-        break;
+        stop = true;
+        return;
       }
       history[(int64_t)b * history_stride + len] = t;
       ++len;
       if (max_tokens && len >= cap) {
         reason = 2;
-        break;
+        stop = true;
       }
-    }
+    };
+#pragma unroll
+    for (int j = 0; j <= kPre; ++j)
+      if (!stop && j <= a) take((int32_t)pv[j]);
+    for (int j = kPre + 1; !stop && j <= a; ++j) take((int32_t)pred[j]);
     history_len[b] = len;
     if (finished) finished[b] = reason;
   }
