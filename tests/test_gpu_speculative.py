@@ -149,9 +149,12 @@ def test_verify_inputs_assembly() -> None:
     assert out.attn_seq_lens.cpu().numpy().tolist() == (seq_len + S).tolist()
 
 
-def test_accept_batch_and_rollback() -> None:
-    rng = np.random.default_rng(13)
-    B, k, S = 64, 3, 4
+@pytest.mark.parametrize("k", [3, 8, 12])
+def test_accept_batch_and_rollback(k: int) -> None:
+    """k = 3 (the benchmark), 8 (the engine's default speculative_tokens, engine.py:121) and 12 (past
+    the kernel's preloaded drafts and predictions)."""
+    rng = np.random.default_rng(13 + k)
+    B, S = 64, k + 1
     draft = rng.integers(0, 5, size=(B, k)).astype(np.int32)
     dlen = rng.integers(0, k + 1, size=B).astype(np.int32)
     for b in range(B):
