@@ -119,6 +119,28 @@ def test_long_histories() -> None:
     assert got[1] == far[104:107].tolist()
 
 
+def test_histories_across_scan_chunks() -> None:
+    """Histories around the kernel's 4096-candidate LDS chunks: the only, or the longest, match sits
+    just before or just after a chunk edge, and a shorter match in a later chunk must not win over
+    a longer one in an earlier-scanned (later) chunk or the reverse."""
+    rng = np.random.default_rng(17)
+    rows = []
+    for L in (4095, 4096, 4097, 4105, 8193):
+        base = rng.permutation(workloads.VOCAB)[:L].astype(np.int32)
+        for p in (L - 4096 - 1, L - 4096, L - 4096 + 1, L - 4096 + 7):  # candidate positions at the edge
+            if 4 <= p <= L - 5:
+                r = base.copy()
+                r[p - 4 : p] = r[-4:]  # a full 4-token match ending just before p
+                rows.append(r.tolist())
+        r = base.copy()
+        r[L - 4096 + 40 - 2 : L - 4096 + 40] = r[-2:]  # 2-token match in the last-scanned chunk
+        r[10:13] = r[-3:]  # longer (3-token) match near the start
+        rows.append(r.tolist())
+    announce("chunk-edge histories", len(rows))
+    got, _, _ = _gpu_drafts(rows, 3, 4)
+    assert got == [ngram.propose_closed_form(r, 3, 4) for r in rows]
+
+
 def test_verify_inputs_assembly() -> None:
     rng = np.random.default_rng(11)
     B, k, S, bs = 8, 3, 4, 16
