@@ -314,6 +314,42 @@ def test_lm_head_wide_ties_take_lowest_index() -> None:
     assert np.array_equal(pred.cpu().numpy(), oracle_lm_head.argmax(_bits(logits)))
 
 
+@pytest.mark.parametrize("rows,vocab,k", [(256, 151_936, 2048), (200, 20_000 + 24, 1024), (129, 1000 + 8, 512)])
+def test_lm_head_256_rows_match_smaller_launches(rows, vocab, k) -> None:
+    """129..256 token rows (8 token tiles per wave) give, row for row, the same bf16 logits and ids as
+    two launches of half the rows (2 or 4 token tiles per wave): every launch sums each logit over k in
+    the same order of 32x32x16 products.  Vocab sizes that leave a partial last tile and workgroups
+    whose last group has fewer tiles than waves; hidden 512, 1024 and 2048."""
+    g = torch.Generator(device="cuda").manual_seed(rows + vocab)
+    hidden, weight = _rand(g, rows, k), _rand(g, vocab, k, std=0.02)
+    weight[vocab - 1] = (hidden[rows - 1].float() * 0.05).to(torch.bfloat16)  # last row's max in the last tile
+    packed = gemm.pack_weight(weight)
+    half = rows // 2
+    announce("lm head 256 rows vs halves", rows, vocab, k)
+    pred, logits = lm_head.lm_head_argmax(hidden, packed, return_logits=True)
+    pa, la = lm_head.lm_head_argmax(hidden[:half].contiguous(), packed, return_logits=True)
+    pb, lb = lm_head.lm_head_argmax(hidden[half:].contiguous(), packed, return_logits=True)
+    torch.cuda.synchronize()
+    assert int(pred[rows - 1]) == vocab - 1
+    assert torch.equal(logits.view(torch.int16), torch.cat([la, lb]).view(torch.int16))
+    assert torch.equal(pred, torch.cat([pa, pb]))
+    assert np.array_equal(pred.cpu().numpy(), oracle_lm_head.argmax(_bits(logits)))
+
+
+def test_lm_head_256_rows_ties_take_lowest_index() -> None:
+    g = torch.Generator(device="cuda").manual_seed(43)
+    vocab, k = 20_000, 1024
+    hidden, weight = _rand(g, 256, k), _rand(g, vocab, k, std=0.02)
+    top = (hidden[200].float() * 0.05).to(torch.bfloat16)
+    for v in (19_999, 8_000, 33, 7):  # different vocab tiles, waves and workgroups: the lowest wins
+        weight[v] = top
+    announce("lm head 256 rows ties")
+    pred, logits = lm_head.lm_head_argmax(hidden, gemm.pack_weight(weight), return_logits=True)
+    torch.cuda.synchronize()
+    assert int(pred[200]) == 7
+    assert np.array_equal(pred.cpu().numpy(), oracle_lm_head.argmax(_bits(logits)))
+
+
 def test_lm_head_ties_take_lowest_index() -> None:
     g = torch.Generator(device="cuda").manual_seed(41)
     vocab, k = 4096 + 32, 2048
