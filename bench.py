@@ -355,7 +355,7 @@ def _cpu_model_name() -> str:
 
 def cpu_baseline(config, model, cache, table, histories, seq_lens, args) -> dict:
     """The oracle's torch-CPU restatement of one verify step (oracle/decoder.py) on this host, timed
-    as BASELINE.md plans: 3 warm-ups then the median of 10 steps, at all affinity cores; and at
+    with 3 warm-ups then the median of 10 steps, at all affinity cores; and at
     one thread (the reference engine pins torch to one, engine.py:207) from a bounded sample --
     the same step with its layer stack cut to 1 and to 2 layers (3 warm-ups + 10 timed each),
     whose difference is the cost of one layer, scaled to the model's layer count."""

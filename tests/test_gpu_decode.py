@@ -1,4 +1,4 @@
-"""The one-token decode step (SURVEY's first "next" row) on the gfx950 kernels.
+"""The one-token decode step (decode_graph.py:33-119, attention.py:76-93) on the gfx950 kernels.
 
 - ``attention.paged_decode`` (the drop-in for attention.py:76-93) against the oracle's attention
   with one query per sequence, including contexts shorter than one key tile and block size 256.
