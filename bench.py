@@ -234,8 +234,8 @@ def _time_us(fn, iters: int = 20, per_graph: int = 10) -> float:
 
 
 def time_configs(config, lm_weight, seed: int = 0) -> dict:
-    """The benchmark's per-kernel configurations (the benchmark's configurations 1, 2 and 4) on the GPU path, inputs
-    resident on the device.  Config 3 is the ``roofline`` launch and config 5 the step itself."""
+    """The benchmark's per-kernel configurations 1-4 on the GPU path, inputs resident on the device.  Config 5
+    is the step itself (its fused attention launch is the ``roofline`` line)."""
     rng = np.random.default_rng(seed)
     dev = "cuda"
     res = {}
@@ -286,6 +286,44 @@ def time_configs(config, lm_weight, seed: int = 0) -> dict:
     res["config2_qk_norm_rope_store"] = {"us": us, "bytes": nbytes, "achieved": nbytes / (us * 1e-6) / 1e9,
                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    del kc, vc
+
+    # Config 3: paged verify attention through the attention.paged_extend drop-in (the unfused kernel
+    # pair), B = 8, S = 4, 16/8 heads, contexts U{2048..8192} (including the 4 new tokens), block 16.
+    # Eight batches with the same lengths and disjoint pages from one random permutation of the
+    # 65,536-block pool are replayed in turn, so their K/V (8 x ~170 MB) comes from HBM rather than the
+    # 256 MB Infinity Cache.
+    b3, s3, nb3, bs3 = 8, 4, 65_536, 16
+    pb3 = workloads.paged_batch(rng, b3, s3, (2048, 8192), block_size=bs3, num_blocks=nb3)
+    need = (pb3.seq_lens + bs3 - 1) // bs3
+    width = int(need.max())
+    perm = rng.permutation(nb3).astype(np.int32)
+    tables, off = [], 0
+    for _ in range(8):
+        tb = np.zeros((b3, width), dtype=np.int32)
+        for bi in range(b3):
+            tb[bi, : need[bi]] = perm[off : off + need[bi]]
+            off += int(need[bi])
+        tables.append(torch.from_numpy(tb).to(dev))
+    kc = torch.randn(nb3, bs3, kv, d, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(nb3, bs3, kv, d, device=dev, dtype=torch.bfloat16)
+    q3 = torch.randn(b3, s3, h, d, device=dev).to(torch.bfloat16)
+    out3 = torch.empty_like(q3)
+    lens3 = torch.from_numpy(pb3.seq_lens).to(dev)
+    ws3 = torch.empty(max(attention.workspace_bytes(b3, kv, width * bs3), 1), dtype=torch.uint8, device=dev)
+    turn = [0]
+
+    def config3_launch():
+        turn[0] = (turn[0] + 1) % len(tables)
+        attention.paged_extend(q3, kc, vc, lens3, tables[turn[0]], max_seq_len=width * bs3, out=out3,
+                               workspace=ws3)
+
+    us3 = _time_us(config3_launch, per_graph=8)
+    bytes3 = int(pb3.seq_lens.astype(np.int64).sum()) * kv * d * 2 * 2 + 2 * q3.numel() * 2
+    res["config3_paged_attention"] = {
+        "us": us3, "bytes": bytes3, "achieved": bytes3 / (us3 * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": bytes3 / (us3 * 1e-6) / 1e9 / HBM_PEAK_GBS, "batch": b3, "tokens_per_seq": s3,
+        "seq_lens": pb3.seq_lens.tolist()}
     del kc, vc
 
     # Config 4: LM head + vocab argmax over 64 sequences x 4 positions, then acceptance (k = 3).
@@ -434,7 +472,7 @@ def main() -> int:
     p.add_argument("--pmc-driver", action="store_true", help="only attention launches + a calibration copy")
     p.add_argument("--cpu-warmup", type=int, default=3)
     p.add_argument("--prefill-driver", action="store_true", help="only the prefill attention measurement")
-    p.add_argument("--configs-driver", action="store_true", help="only the per-kernel configurations 1, 2 and 4")
+    p.add_argument("--configs-driver", action="store_true", help="only the per-kernel configurations 1-4")
     args = p.parse_args()
     if args.ctx_min is not None and not 1 <= args.ctx_min <= args.ctx:
         p.error("--ctx-min must be in [1, --ctx]")

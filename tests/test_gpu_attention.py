@@ -72,6 +72,15 @@ def test_ragged_contexts(seq_lens) -> None:
     _run(seq_lens, 4, 16, 8, 16, 4096, seed=32)
 
 
+@pytest.mark.parametrize("seq_lens", [[5, 33, 16000, 700, 4096, 12000, 64, 2048], [16000, 40], [20000]])
+def test_widely_mixed_contexts(seq_lens) -> None:
+    """Contexts of very different lengths in one launch (each cut into the launch's split count):
+    contexts that fit one split, stored directly, beside others that are merged; a batch of two with
+    32 splits each; and one 20,000-key context over 64 splits."""
+    announce("attention mixed contexts", seq_lens)
+    _run(seq_lens, 4, 16, 8, 16, 4096, seed=37)
+
+
 def test_reference_block_size_256_and_table_slack() -> None:
     announce("attention block 256")
     _run([300, 700, 40], 4, 16, 8, 256, 64, seed=33, table_width=8)
