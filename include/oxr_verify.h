@@ -243,14 +243,52 @@ int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight,
                                   oxr_stream_t stream);
 
 /*
+ * (3c) Balanced context pieces for (3) and (3b).  No counterpart in the
+ * reference (its flash-attn kernel schedules work itself); for batches whose
+ * contexts differ in length, where (3) and (3b) cut every context into the
+ * same number of pieces and the longest context bounds the launch.
+ * oxr_paged_extend_plan writes, on the stream, a plan of
+ * oxr_paged_extend_plan_ints(...) int32 entries from the device seq_lens (the
+ * arguments are those of the launch the plan is for; 0 entries: the launch
+ * keeps every context in one piece and needs no plan).  The planned launches
+ * take the plan written for the same seq_lens, batch, tokens_per_seq, heads
+ * and max_seq_len: every context is cut into pieces of about the batch's mean
+ * share, long contexts taking the workgroups short ones leave spare (each
+ * workgroup keeps its partials in its own slot of the same workspace).  Same
+ * arguments, requirements and workspace as (3) and (3b) otherwise; outputs
+ * within the same tolerance (the pieces differ, so the fp32 merge order does),
+ * and the planned (3b) is bit-identical to the planned (3).
+ */
+size_t oxr_paged_extend_plan_ints(int32_t batch, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
+                                  int32_t max_seq_len);
+int oxr_paged_extend_plan(const int32_t* seq_lens, int32_t batch, int32_t tokens_per_seq, int32_t num_heads,
+                          int32_t num_kv_heads, int32_t max_seq_len, int32_t* plan, size_t plan_ints,
+                          oxr_stream_t stream);
+int oxr_paged_extend_planned(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache,
+                             const int32_t* seq_lens, const int32_t* block_table, int64_t table_stride, int32_t batch,
+                             int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
+                             void* workspace, size_t workspace_bytes, const int32_t* plan, oxr_stream_t stream);
+int oxr_qk_norm_rope_paged_extend_planned(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
+                                          const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,
+                                          const int64_t* positions, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache,
+                                          const int64_t* slots, int64_t num_slots, const int32_t* seq_lens,
+                                          const int32_t* block_table, int64_t table_stride, int32_t batch,
+                                          int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
+                                          int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                          int32_t max_seq_len, float scale, oxr_bf16* out, int32_t out_packed,
+                                          void* workspace, size_t workspace_bytes, const int32_t* plan,
+                                          oxr_stream_t stream);
+
+/*
  * (3b') (3b) without a workspace argument, allocating nothing.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops or harnesses that forbid allocation).
  * The split partials live in a static device array of
  * oxr_static_scratch_bytes() bytes (16.25 MiB) that each GPU the library runs
  * on holds until the process ends.  Every shape (3b) accepts fits it (a launch
- * splits contexts into at most 1020 partial units); a shape whose
- * oxr_paged_extend_workspace_bytes exceeded it would return
+ * splits contexts into at most 1020 partial units); a shape whose partials
+ * exceeded it would return
  * OXR_ERR_SCRATCH_LIMIT.  The array's device address is looked
  * up on the first call on each device, which must therefore not be inside a
  * stream capture.  All calls on one GPU share the array: calls that overlap in

@@ -19,10 +19,39 @@ def workspace_bytes(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
     return int(_lib.lib().oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len))
 
 
+def plan_ints(batch: int, tokens_per_seq: int, num_heads: int, num_kv_heads: int, max_seq_len: int) -> int:
+    """int32 entries of a context-piece plan (:func:`build_plan`) for these launch parameters; 0 when
+    the launch keeps every context in one piece."""
+    return int(_lib.lib().oxr_paged_extend_plan_ints(batch, tokens_per_seq, num_heads, num_kv_heads, max_seq_len))
+
+
+def build_plan(seq_lens: torch.Tensor, tokens_per_seq: int, num_heads: int, num_kv_heads: int, max_seq_len: int,
+               *, out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """Balanced context pieces for a :func:`paged_extend` / :func:`qk_norm_rope_paged_extend` launch over
+    ``seq_lens`` (device int32 [B]), written on the device (so under graph capture it follows the
+    lengths of each replay).  Without a plan every context is cut into the same number of pieces and
+    the longest context bounds the launch; with one, pieces are about the batch's mean share and long
+    contexts take the workgroups short ones leave.  Pass the result as ``plan=`` to a launch with the
+    same lengths, batch, tokens_per_seq, heads and max_seq_len.  None when no plan is needed."""
+    device = _lib.require_gpu(seq_lens, name="build_plan")
+    _lib.require(seq_lens.dtype == torch.int32 and seq_lens.dim() == 1 and seq_lens.is_contiguous(),
+                 "seq_lens must be contiguous int32 [B]")
+    b = seq_lens.shape[0]
+    n = plan_ints(b, tokens_per_seq, num_heads, num_kv_heads, max_seq_len)
+    if n == 0:
+        return None
+    if out is None:
+        out = torch.empty(n, dtype=torch.int32, device=device)
+    _lib.require(out.dtype == torch.int32 and out.is_contiguous() and out.numel() >= n, "build_plan: out too small")
+    _lib.call("oxr_paged_extend_plan", seq_lens.data_ptr(), b, tokens_per_seq, num_heads, num_kv_heads, max_seq_len,
+              out.data_ptr(), out.numel(), _lib.stream(device))
+    return out
+
+
 def paged_extend(
     q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seq_lens: torch.Tensor,
     block_table: torch.Tensor, *, scale: float | None = None, max_seq_len: int | None = None,
-    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, plan: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Each sequence brings S new tokens (``q`` is ``[B, S, heads, dim]``; their K/V are already in the
     paged cache); token j sees itself and everything before it (``seq_lens`` includes the S tokens).
@@ -30,7 +59,7 @@ def paged_extend(
 
     ``max_seq_len`` bounds every ``seq_lens[b]`` (default: the block table's span) and sizes the
     context split; ``out`` and ``workspace`` (bytes from :func:`workspace_bytes`) may be passed in to
-    avoid allocations."""
+    avoid allocations; ``plan`` (from :func:`build_plan`) balances contexts of different lengths."""
     device = _lib.require_gpu(q, k_cache, v_cache, seq_lens, block_table, name="paged_extend")
     _lib.require(q.dim() == 4 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [B, S, H, D]")
     b, s, h, d = q.shape
@@ -53,13 +82,20 @@ def paged_extend(
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
     _lib.require(workspace.numel() * workspace.element_size() >= need, "paged_extend: workspace too small")
-    _lib.call(
-        "oxr_paged_extend", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), seq_lens.data_ptr(),
-        block_table.data_ptr(), block_table.stride(0), b, s, h, kv, d, block_size, num_blocks, max_seq_len,
-        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-        _lib.stream(device),
-    )
+    args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
+            block_table.stride(0), b, s, h, kv, d, block_size, num_blocks, max_seq_len, float(scale), out.data_ptr(),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    if plan is None:
+        _lib.call("oxr_paged_extend", *args, _lib.stream(device))
+    else:
+        _check_plan(plan, b, s, h, kv, max_seq_len, device)
+        _lib.call("oxr_paged_extend_planned", *args, plan.data_ptr(), _lib.stream(device))
     return out
+
+
+def _check_plan(plan: torch.Tensor, b: int, s: int, h: int, kv: int, max_seq_len: int, device) -> None:
+    _lib.require(plan.device == device and plan.dtype == torch.int32 and plan.is_contiguous()
+                 and plan.numel() >= plan_ints(b, s, h, kv, max_seq_len), "plan: int32 from build_plan for this launch")
 
 
 def varlen(
@@ -113,7 +149,7 @@ def qk_norm_rope_paged_extend(
     sin_table: torch.Tensor, positions: torch.Tensor, eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
     slots: torch.Tensor, seq_lens: torch.Tensor, block_table: torch.Tensor, num_heads: int, *,
     scale: float | None = None, max_seq_len: int | None = None, out: torch.Tensor | PackedMatrix | None = None,
-    workspace: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None, plan: torch.Tensor | None = None,
 ) -> torch.Tensor | PackedMatrix:
     """The decoder layer's attention block of the verify step (oxr_runtime/language.py:311-316) in one
     launch: ``kernels.qk_norm_rope_store`` (q/k RMSNorm + RoPE at ``positions``, K/V into the cache at
@@ -153,12 +189,14 @@ def qk_norm_rope_paged_extend(
     need = workspace_bytes(b, kv, max_seq_len)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
-    _lib.call(
-        "oxr_qk_norm_rope_paged_extend", qkv.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(),
-        cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0], positions.data_ptr(), float(eps),
-        k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), num_blocks * block_size, seq_lens.data_ptr(),
-        block_table.data_ptr(), block_table.stride(0), b, s, num_heads, kv, d, block_size, num_blocks, max_seq_len,
-        float(scale), out_t.data_ptr(), 1 if packed else 0, workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), _lib.stream(device),
-    )
+    args = (qkv.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+            cos_table.shape[0], positions.data_ptr(), float(eps), k_cache.data_ptr(), v_cache.data_ptr(),
+            slots.data_ptr(), num_blocks * block_size, seq_lens.data_ptr(), block_table.data_ptr(),
+            block_table.stride(0), b, s, num_heads, kv, d, block_size, num_blocks, max_seq_len, float(scale),
+            out_t.data_ptr(), 1 if packed else 0, workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    if plan is None:
+        _lib.call("oxr_qk_norm_rope_paged_extend", *args, _lib.stream(device))
+    else:
+        _check_plan(plan, b, s, num_heads, kv, max_seq_len, device)
+        _lib.call("oxr_qk_norm_rope_paged_extend_planned", *args, plan.data_ptr(), _lib.stream(device))
     return out

@@ -153,6 +153,7 @@ constexpr int kMaxRowTiles = 2;      // 16-row MFMA tiles of query rows per (seq
 constexpr int kPartRows = 16 * kMaxRowTiles;  // row stride of the split partials
 constexpr int kMaxNew = 16;          // new tokens per sequence (S) of the fused kernel
 constexpr int kJobSlots = 64 * kWaves / 16;   // 16-lane row jobs per round of the fused prologue
+constexpr int kPlanHead = 2;         // plan: [valid, splits, pieces per sequence..., slot entries...]
 
 // Inputs of the fused q/k norm + RoPE + KV store (oxr_qk_norm_rope_paged_extend).
 struct RopeArgs {
@@ -178,12 +179,13 @@ struct RopeArgs {
 // NT: 16-row tiles of query rows (R = S * H / KV <= 16 * NT); every pair of keys
 // is multiplied by each tile, and the V^T fragments are shared by the tiles.
 // JR: rounds of the fused prologue's 32 row jobs (HPW * (R + 2 S) <= 32 * JR).
-template <bool kFused, int HPW, int NT, int JR>
+// kPlanned: pieces from a plan (paged_extend_plan_kernel); otherwise `splits` even pieces per context.
+template <bool kFused, int HPW, int NT, int JR, bool kPlanned>
 __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
     const bf16_t* __restrict__ q, const bf16_t* k_cache, const bf16_t* v_cache, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ block_table, int64_t table_stride, int S, int H, int KV, int log2_bs,
-    int64_t num_blocks, float scale_log2, int max_seq_len, int splits, float* __restrict__ part_o,
-    float* __restrict__ part_ml, bf16_t* __restrict__ out, int out_packed, RopeArgs ra) {
+    int64_t num_blocks, float scale_log2, int max_seq_len, int splits, const int32_t* __restrict__ plan,
+    float* __restrict__ part_o, float* __restrict__ part_ml, bf16_t* __restrict__ out, int out_packed, RopeArgs ra) {
   constexpr int kStreams = kWaves / HPW;  // waves per kv head
   // Two row tiles' q fragments (32 registers) would not fit next to two tiles'
   // accumulators and the two pair buffers: with NT = 2 the MFMAs read them from LDS.
@@ -195,7 +197,18 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ int s_pages[kMaxSpanPages];
 
-  const int split = blockIdx.x, b = blockIdx.z;
+  // Which piece of which context this workgroup takes: piece blockIdx.x of sequence blockIdx.z of
+  // `splits` even pieces, or, with a plan (paged_extend_plan_kernel), the entry of its slot.
+  int split = blockIdx.x, b = blockIdx.z, pieces = 0;
+  if constexpr (kPlanned) {
+    const int a = plan[kPlanHead + gridDim.z + blockIdx.z * splits + blockIdx.x];
+    // A spare slot the plan leaves idle (workgroup-uniform); entries out of range (a plan written for
+    // another launch) are treated alike, so nothing is addressed outside the launch's arrays.
+    if (a < 0 || (a >> 8) >= (int)gridDim.z || (a & 255) >= 2 * splits) return;
+    b = a >> 8;
+    split = a & 255;
+    pieces = min(max(plan[kPlanHead + b], 1), 2 * splits);
+  }
   const int G = H / KV, R = S * G;
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, so its addressing is scalar
@@ -254,11 +267,15 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 
   const int L = min(seq_lens[b], max_seq_len);  // max_seq_len <= table span, checked on the host
 
-  // This workgroup's keys: split `split` of [0, L), in whole 32-key pairs.
-  const int span = ((L + splits - 1) / splits + 31) / 32 * 32;
+  // This workgroup's keys: piece `split` of [0, L), in whole 32-key pairs.
+  // (A plan's pieces are never longer than an even split of max_seq_len; the clamp keeps the page
+  // range inside the LDS copy whatever the plan holds.)
+  const int span = kPlanned ? min(((L + pieces - 1) / pieces + 31) / 32 * 32,
+                                  ((max_seq_len + splits - 1) / splits + 31) / 32 * 32)
+                            : ((L + splits - 1) / splits + 31) / 32 * 32;
   const int t_begin = split * span;
   const int t_end = min(L, t_begin + span);
-  const bool single = L <= span;  // the whole context is in split 0
+  const bool single = kPlanned ? pieces == 1 : L <= span;  // the whole context is in piece 0
   if (single && split > 0) return;
   const int32_t* table_row = block_table + (int64_t)b * table_stride;
 
@@ -519,7 +536,9 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
       const int ho = idx / (rows * (kD / 4)), rl = (idx / (kD / 4)) % rows, d0 = (idx % (kD / 4)) * 4;
       const int rr = 16 * t + rl;
       const int kvh_o = (int)blockIdx.y * HPW + ho;
-      const int64_t unit0 = ((int64_t)b * KV + kvh_o) * splits;
+      // Even: the (sequence, piece) unit; planned: this workgroup's own slot (the plan maps pieces to slots).
+      const int64_t unit = kPlanned ? ((int64_t)blockIdx.z * KV + kvh_o) * splits + blockIdx.x
+                                    : ((int64_t)b * KV + kvh_o) * splits + split;
       float mmax = -INFINITY;
 #pragma unroll
       for (int k = 0; k < kStreams; ++k) mmax = fmaxf(mmax, s_m[ho + HPW * k][rl]);
@@ -540,28 +559,83 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
         dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
       } else {
-        f32x4* const po = reinterpret_cast<f32x4*>(part_o + ((unit0 + split) * kPartRows + rr) * kD + d0);
+        f32x4* const po = reinterpret_cast<f32x4*>(part_o + (unit * kPartRows + rr) * kD + d0);
         *po = acc;
-        if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + ((unit0 + split) * kPartRows + rr) * 2) = f32x2{mmax, l};
+        if (d0 == 0) *reinterpret_cast<f32x2*>(part_ml + (unit * kPartRows + rr) * 2) = f32x2{mmax, l};
       }
     }
   }
 }
 
+// The merge for a planned launch: the sequence's context is in `pieces` pieces, piece j's partial at the
+// unit of the workgroup slot piece_slots[j] (z << 8 | x) names (each written by this launch, possibly
+// empty: max -inf, sum 0); one piece was stored by the main kernel.  All of a chunk's partials are
+// requested before the first use.
+__device__ __forceinline__ void merge_planned(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                              int pieces, const int32_t* __restrict__ piece_slots, int b, int KV,
+                                              int kvh, int splits, int rr, int d0, uint32_t* dst) {
+  constexpr int kChunk = 8;
+  if (pieces <= 1) return;
+  float m = -INFINITY, l = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < pieces; c0 += kChunk) {
+    f32x2 ml[kChunk];
+    f32x4 v[kChunk];
+    int64_t unit[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {  // past the last piece: the last, weight 0 below
+      const int jj = min(c0 + j, pieces - 1);
+      // The first `splits` pieces sit in the sequence's own slots; later ones in the slots that took them.
+      const int e = jj < splits ? (b << 8) | jj : piece_slots[jj];
+      unit[j] = ((int64_t)(e >> 8) * KV + kvh) * splits + (e & 255);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const int64_t u = unit[j];
+      ml[j] = *reinterpret_cast<const f32x2*>(part_ml + (u * kPartRows + rr) * 2);
+      v[j] = *reinterpret_cast<const f32x4*>(part_o + (u * kPartRows + rr) * kD + d0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const float mj = c0 + j < pieces ? ml[j][0] : -INFINITY;
+      const float mn = fmaxf(m, mj);
+      const float mu = (mn == -INFINITY) ? 0.f : mn;
+      const float a = exp2f(m - mu), w = exp2f(mj - mu);
+      l = l * a + ml[j][1] * w;
+      acc = acc * a + v[j] * w;
+      m = mn;
+    }
+  }
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
+  dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
+}
+
 // Merge of the context splits of every (sequence, kv head): one workgroup per
 // pair, one thread per 4 output dims of a row.  Sequences whose context fitted
 // one split were already stored by the main kernel.
+template <bool kPlanned>
 __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(const float* __restrict__ part_o,
                                                                               const float* __restrict__ part_ml,
                                                                               const int32_t* __restrict__ seq_lens,
                                                                               int S, int H, int KV, int max_seq_len,
-                                                                              int splits, bf16_t* __restrict__ out,
+                                                                              int splits,
+                                                                              const int32_t* __restrict__ plan,
+                                                                              bf16_t* __restrict__ out,
                                                                               int out_packed) {
   constexpr int kChunk = 8;  // splits whose partials are requested together
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int G = H / KV;
   // One thread per 4 output dims of a row (blockDim = rows * 32).
   const int rr = threadIdx.x / (kD / 4), d0 = (threadIdx.x % (kD / 4)) * 4;
+  if constexpr (kPlanned) {
+    const int pieces = min(max(plan[kPlanHead + b], 1), 2 * splits);
+    merge_planned(part_o, part_ml, pieces, plan + kPlanHead + (int)gridDim.y * (1 + splits) + b * 2 * splits, b,
+                  KV, kvh, splits, rr, d0,
+                  out_vec(out, (int64_t)b * S + rr / G, (kvh * G + rr % G) * kD + d0, H * kD, out_packed));
+    return;
+  }
   const int64_t unit0 = ((int64_t)b * KV + kvh) * splits;
   // The context length is only needed at the end, but it is requested first so that its
   // latency overlaps the partials' instead of following it.  (As inline asm: the compiler
@@ -607,6 +681,90 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
   dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
 }
 
+// A plan of context pieces for one launch (oxr_paged_extend_plan), so that contexts of different
+// lengths take workgroups in proportion.  Without one, every context is cut into the launch's
+// `splits` pieces and the longest bounds the launch.  One piece length serves the whole batch:
+// the smallest multiple of 32 keys, from its total context over the B * splits workgroup slots up,
+// for which the pieces fit the slots (each context at least one piece, at most 2 * splits).
+// Slot (sequence z, x) takes piece x of context z while z has that many; the slots a short
+// context leaves spare take, in order, the pieces past `splits` of the long ones; any left over
+// stay idle.  Layout: [1, splits, pieces of each sequence (B), slot entries (B * splits): sequence << 8 |
+// piece, or -1 for idle; then per sequence 2 * splits piece entries: the slot z << 8 | x that takes the
+// piece (-1 past the sequence's pieces)].  A workgroup writes its partial at its own slot's unit, so
+// the workspace is that of an even launch.
+constexpr int kPlanMaxBatch = 256;
+constexpr int kPlanThreads = 256;
+__global__ __launch_bounds__(kPlanThreads) void paged_extend_plan_kernel(const int32_t* __restrict__ seq_lens,
+                                                                         int batch, int max_seq_len, int splits,
+                                                                         int32_t* __restrict__ plan) {
+  __shared__ int s_len[kPlanMaxBatch], s_n[kPlanMaxBatch];
+  __shared__ int s_spare[kPlanMaxBatch + 1], s_over[kPlanMaxBatch + 1];  // exclusive prefix sums
+  __shared__ unsigned long long s_total;
+  __shared__ int s_count;
+  const int t = threadIdx.x;
+  const int len = t < batch ? max(0, min(seq_lens[t], max_seq_len)) : 0;
+  if (t < batch) s_len[t] = len;
+  if (t == 0) s_total = 0ull;
+  __syncthreads();
+  if (len > 0) atomicAdd(&s_total, (unsigned long long)len);
+  __syncthreads();
+  const long long slots = (long long)batch * splits;
+  const long long total = (long long)s_total;
+  int span = (int)((total + slots - 1) / slots);
+  span = max(32, (span + 31) / 32 * 32);
+  const int span_max = max(32, (max_seq_len + 31) / 32 * 32);  // one piece per context: always fits
+  for (int it = 0; it < 1 << 16; ++it) {
+    if (t == 0) s_count = 0;
+    __syncthreads();
+    if (t < batch) atomicAdd(&s_count, min(max((len + span - 1) / span, 1), 2 * splits));
+    __syncthreads();
+    const int count = s_count;
+    __syncthreads();  // every thread has read the count before the next pass clears it
+    if (count <= slots || span >= span_max) break;
+    span += 32;
+  }
+  if (t < batch) s_n[t] = min(max((len + span - 1) / span, 1), 2 * splits);
+  __syncthreads();
+  if (t == 0) {
+    int sp = 0, ov = 0;
+    for (int b = 0; b < batch; ++b) {
+      s_spare[b] = sp;
+      s_over[b] = ov;
+      sp += splits - min(s_n[b], splits);
+      ov += max(s_n[b] - splits, 0);
+    }
+    s_spare[batch] = sp;
+    s_over[batch] = ov;
+    plan[0] = 1;
+    plan[1] = splits;
+  }
+  __syncthreads();
+  if (t < batch) plan[kPlanHead + t] = s_n[t];
+  for (long long w = t; w < slots; w += kPlanThreads) {
+    const int z = (int)(w / splits), x = (int)(w % splits);
+    int entry = -1;
+    if (x < s_n[z]) {
+      entry = (z << 8) | x;
+    } else {
+      const int r = s_spare[z] + (x - s_n[z]);  // rank among the spare slots
+      if (r < s_over[batch]) {                  // the overflow piece of that rank
+        int lo = 0, hi = batch;                 // s_over[lo] <= r < s_over[lo + 1]
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) / 2;
+          if (s_over[mid] <= r) lo = mid;
+          else hi = mid;
+        }
+        entry = (lo << 8) | (splits + (r - s_over[lo]));
+      }
+    }
+    plan[kPlanHead + batch + w] = entry;
+    if (entry >= 0) plan[kPlanHead + batch + slots + (entry >> 8) * 2 * splits + (entry & 255)] = (z << 8) | x;
+  }
+  // Piece entries past each sequence's pieces.
+  for (long long e = t; e < (long long)batch * 2 * splits; e += kPlanThreads)
+    if ((int)(e % (2 * splits)) >= s_n[e / (2 * splits)]) plan[kPlanHead + batch + slots + e] = -1;
+}
+
 // Context splits per (sequence, group of `hpw` kv heads): about one 8-wave
 // workgroup per CU over the whole batch, but at least kMinSplitKeys keys of
 // the longest context per split.  (At B = 1, 256 workgroups would leave 64
@@ -644,13 +802,15 @@ int job_rounds(int hpw, int32_t tokens_per_seq, int32_t num_heads, int32_t num_k
 }  // namespace
 }  // namespace oxr
 
-extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
-  using namespace oxr;
+namespace oxr {
+namespace {
+
+// Bytes of split partials a launch needs: the largest (batch' * KV * splits) over any head grouping and
+// any batch' <= batch (smaller batches split their contexts further, so a workspace sized for a batch
+// serves every smaller one).  A planned launch writes one partial per workgroup slot too.  (A launch
+// with one split stores its output directly and needs none.)
+size_t partial_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
   if (batch <= 0 || num_kv_heads <= 0 || max_seq_len <= 0) return 0;
-  // Partials of the largest (batch' * KV * splits) over any head grouping and any batch' <= batch:
-  // smaller batches split their contexts further, and a workspace sized for a batch serves every
-  // smaller one.
-  // (A launch with one split stores its output directly and needs none.)
   size_t units = 0;
   for (int32_t bb = 1; bb <= batch; ++bb)
     for (int hpw : {1, 2})
@@ -659,6 +819,13 @@ extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv
         if (splits > 1) units = std::max(units, (size_t)bb * num_kv_heads * splits);
       }
   return units * kPartRows * (kD + 2) * sizeof(float);
+}
+
+}  // namespace
+}  // namespace oxr
+
+extern "C" size_t oxr_paged_extend_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
+  return oxr::partial_bytes(batch, num_kv_heads, max_seq_len);
 }
 
 namespace oxr {
@@ -670,7 +837,8 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
                         const int32_t* block_table, int64_t table_stride, int32_t batch, int32_t tokens_per_seq,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                         int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out, int out_packed,
-                        void* workspace, size_t workspace_bytes, const RopeArgs* ra, hipStream_t s) {
+                        void* workspace, size_t workspace_bytes, const RopeArgs* ra, const int32_t* plan,
+                        hipStream_t s) {
   OXR_RETURN_IF(batch < 0 || tokens_per_seq <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
                     table_stride < 0 || max_seq_len <= 0,
                 OXR_ERR_INVALID_ARG);
@@ -681,7 +849,7 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   OXR_RETURN_IF((int64_t)max_seq_len > table_stride * block_size, OXR_ERR_INVALID_ARG);
   if (batch == 0) return OXR_OK;
   OXR_RETURN_IF((!ra && !q) || !k_cache || !v_cache || !seq_lens || !block_table || !out, OXR_ERR_INVALID_ARG);
-  const size_t need = oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len);
+  const size_t need = partial_bytes(batch, num_kv_heads, max_seq_len);
   OXR_RETURN_IF((need > 0 && !workspace) || workspace_bytes < need, OXR_ERR_WORKSPACE);
   OXR_RETURN_IF(batch > 65535 || num_kv_heads > 65535 || num_blocks > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
   const int hpw = pick_hpw(tokens_per_seq, num_heads, num_kv_heads);
@@ -694,6 +862,7 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   int log2_bs = 0;
   while ((1 << log2_bs) < block_size) ++log2_bs;
   float* part_o = static_cast<float*>(workspace);
+  if (splits == 1) plan = nullptr;  // nothing to balance: every context is one piece
   float* part_ml = part_o + (size_t)batch * num_kv_heads * splits * kPartRows * kD;
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(splits, num_kv_heads / hpw, batch), block(64 * kWaves);
@@ -701,33 +870,38 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, block, 0, s, ra ? nullptr : q, k_cache, v_cache, seq_lens, block_table,
                        table_stride, tokens_per_seq, num_heads, num_kv_heads, log2_bs, num_blocks, scale_log2,
-                       max_seq_len, splits, part_o, part_ml, out, out_packed, rope);
+                       max_seq_len, splits, plan, part_o, part_ml, out, out_packed, rope);
+  };  auto launch_k = [&](auto even, auto planned) {
+    if (plan) launch(planned);
+    else launch(even);
   };
+
   const int nt = tokens_per_seq * (num_heads / num_kv_heads) > 16 ? 2 : 1;
   if (ra) {
     const int jr = job_rounds(hpw, tokens_per_seq, num_heads, num_kv_heads);  // 1 or 2, checked by the caller
     switch ((hpw - 1) * 4 + (nt - 1) * 2 + (jr - 1)) {
-      case 0: launch(paged_extend_kernel<true, 1, 1, 1>); break;
-      case 1: launch(paged_extend_kernel<true, 1, 1, 2>); break;
-      case 2: launch(paged_extend_kernel<true, 1, 2, 1>); break;
-      case 3: launch(paged_extend_kernel<true, 1, 2, 2>); break;
-      case 4: launch(paged_extend_kernel<true, 2, 1, 1>); break;
-      case 6: launch(paged_extend_kernel<true, 2, 2, 1>); break;
+      case 0: launch_k(paged_extend_kernel<true, 1, 1, 1, false>, paged_extend_kernel<true, 1, 1, 1, true>); break;
+      case 1: launch_k(paged_extend_kernel<true, 1, 1, 2, false>, paged_extend_kernel<true, 1, 1, 2, true>); break;
+      case 2: launch_k(paged_extend_kernel<true, 1, 2, 1, false>, paged_extend_kernel<true, 1, 2, 1, true>); break;
+      case 3: launch_k(paged_extend_kernel<true, 1, 2, 2, false>, paged_extend_kernel<true, 1, 2, 2, true>); break;
+      case 4: launch_k(paged_extend_kernel<true, 2, 1, 1, false>, paged_extend_kernel<true, 2, 1, 1, true>); break;
+      case 6: launch_k(paged_extend_kernel<true, 2, 2, 1, false>, paged_extend_kernel<true, 2, 2, 1, true>); break;
       default: return OXR_ERR_UNSUPPORTED;  // two heads are only chosen when one round holds their jobs
     }
   } else {
     switch ((hpw - 1) * 2 + (nt - 1)) {
-      case 0: launch(paged_extend_kernel<false, 1, 1, 1>); break;
-      case 1: launch(paged_extend_kernel<false, 1, 2, 1>); break;
-      case 2: launch(paged_extend_kernel<false, 2, 1, 1>); break;
-      default: launch(paged_extend_kernel<false, 2, 2, 1>); break;
+      case 0: launch_k(paged_extend_kernel<false, 1, 1, 1, false>, paged_extend_kernel<false, 1, 1, 1, true>); break;
+      case 1: launch_k(paged_extend_kernel<false, 1, 2, 1, false>, paged_extend_kernel<false, 1, 2, 1, true>); break;
+      case 2: launch_k(paged_extend_kernel<false, 2, 1, 1, false>, paged_extend_kernel<false, 2, 1, 1, true>); break;
+      default: launch_k(paged_extend_kernel<false, 2, 2, 1, false>, paged_extend_kernel<false, 2, 2, 1, true>); break;
     }
   }
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;
   const int rows = tokens_per_seq * (num_heads / num_kv_heads);
-  hipLaunchKernelGGL(paged_extend_merge_kernel, dim3(num_kv_heads, batch), dim3(rows * kD / 4), 0, s, part_o, part_ml,
-                     seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, out, out_packed);
+  hipLaunchKernelGGL(plan ? paged_extend_merge_kernel<true> : paged_extend_merge_kernel<false>, dim3(num_kv_heads, batch),
+                     dim3(rows * kD / 4), 0, s, part_o, part_ml,
+                     seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, plan, out, out_packed);
   return OXR_LAUNCH_STATUS();
 }
 
@@ -742,7 +916,7 @@ extern "C" int oxr_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, cons
                                 oxr_stream_t stream) {
   return oxr::launch_paged_extend(q, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
                                   num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
-                                  0, workspace, workspace_bytes, nullptr, (hipStream_t)stream);
+                                  0, workspace, workspace_bytes, nullptr, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
@@ -768,7 +942,68 @@ extern "C" int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16
                     k_cache, v_cache};
   return launch_paged_extend(nullptr, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
                              num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
-                             out_packed ? 1 : 0, workspace, workspace_bytes, &ra, (hipStream_t)stream);
+                             out_packed ? 1 : 0, workspace, workspace_bytes, &ra, nullptr, (hipStream_t)stream);
+}
+
+extern "C" size_t oxr_paged_extend_plan_ints(int32_t batch, int32_t tokens_per_seq, int32_t num_heads,
+                                             int32_t num_kv_heads, int32_t max_seq_len) {
+  using namespace oxr;
+  if (batch <= 0 || tokens_per_seq <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_seq_len <= 0 ||
+      num_heads % num_kv_heads != 0)
+    return 0;
+  const int splits = splits_for(batch, num_kv_heads, pick_hpw(tokens_per_seq, num_heads, num_kv_heads), max_seq_len);
+  return splits > 1 ? (size_t)kPlanHead + (size_t)batch + (size_t)batch * 3 * splits : 0;
+}
+
+extern "C" int oxr_paged_extend_plan(const int32_t* seq_lens, int32_t batch, int32_t tokens_per_seq,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t max_seq_len, int32_t* plan,
+                                     size_t plan_ints, oxr_stream_t stream) {
+  using namespace oxr;
+  OXR_RETURN_IF(batch < 0 || tokens_per_seq <= 0 || num_heads <= 0 || num_kv_heads <= 0 || max_seq_len <= 0,
+                OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(num_heads % num_kv_heads != 0, OXR_ERR_UNSUPPORTED);
+  const size_t need = oxr_paged_extend_plan_ints(batch, tokens_per_seq, num_heads, num_kv_heads, max_seq_len);
+  if (need == 0) return OXR_OK;  // one piece per context: a planned launch ignores the plan
+  OXR_RETURN_IF(!seq_lens || !plan || plan_ints < need, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(batch > kPlanMaxBatch, OXR_ERR_UNSUPPORTED);  // not reached: contexts split only below 256 units
+  const int splits = splits_for(batch, num_kv_heads, pick_hpw(tokens_per_seq, num_heads, num_kv_heads), max_seq_len);
+  hipLaunchKernelGGL(paged_extend_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, seq_lens, batch,
+                     max_seq_len, splits, plan);
+  return OXR_LAUNCH_STATUS();
+}
+
+extern "C" int oxr_paged_extend_planned(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf16* v_cache,
+                                        const int32_t* seq_lens, const int32_t* block_table, int64_t table_stride,
+                                        int32_t batch, int32_t tokens_per_seq, int32_t num_heads,
+                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                        int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
+                                        void* workspace, size_t workspace_bytes, const int32_t* plan,
+                                        oxr_stream_t stream) {
+  return oxr::launch_paged_extend(q, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
+                                  num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
+                                  0, workspace, workspace_bytes, nullptr, plan, (hipStream_t)stream);
+}
+
+extern "C" int oxr_qk_norm_rope_paged_extend_planned(
+    const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight, const oxr_bf16* cos_table,
+    const oxr_bf16* sin_table, int64_t table_rows, const int64_t* positions, float eps, oxr_bf16* k_cache,
+    oxr_bf16* v_cache, const int64_t* slots, int64_t num_slots, const int32_t* seq_lens, const int32_t* block_table,
+    int64_t table_stride, int32_t batch, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
+    int32_t out_packed, void* workspace, size_t workspace_bytes, const int32_t* plan, oxr_stream_t stream) {
+  using namespace oxr;
+  OXR_RETURN_IF(num_slots < 0, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+                    (tokens_per_seq > kMaxNew || tokens_per_seq * (num_heads / num_kv_heads + 2) > 2 * kJobSlots),
+                OXR_ERR_UNSUPPORTED);
+  OXR_RETURN_IF(batch > 0 && (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || table_rows <= 0 ||
+                              !positions || !slots),
+                OXR_ERR_INVALID_ARG);
+  const RopeArgs ra{qkv, q_weight, k_weight, cos_table, sin_table, table_rows, positions, slots, num_slots, eps,
+                    k_cache, v_cache};
+  return launch_paged_extend(nullptr, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
+                             num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
+                             out_packed ? 1 : 0, workspace, workspace_bytes, &ra, plan, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -827,7 +1062,7 @@ extern "C" int oxr_qk_norm_rope_paged_extend_static(
     int32_t out_packed, oxr_stream_t stream) {
   using namespace oxr;
   if (batch > 0 && num_kv_heads > 0 && max_seq_len > 0 &&
-      oxr_paged_extend_workspace_bytes(batch, num_kv_heads, max_seq_len) > kScratchBytes)
+      partial_bytes(batch, num_kv_heads, max_seq_len) > kScratchBytes)
     return OXR_ERR_SCRATCH_LIMIT;
   void* ws = nullptr;
   const int st = scratch_address(&ws);

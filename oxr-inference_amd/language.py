@@ -243,6 +243,10 @@ class StepBuffers:
     max_seq_len: int
     max_batch: int = field(default=0)
     pending_splits: int = field(default=0)  # partials not yet added to the residual (0: none)
+    # Context-piece plan of the attention launches (attention.build_plan), rebuilt from the step's
+    # seq_lens at the start of run_layers when `balanced` is set (contexts of different lengths).
+    attn_plan: torch.Tensor | None = field(default=None)
+    balanced: bool = field(default=False)
 
     @classmethod
     def allocate(cls, config: LanguageConfig, max_batch: int, tokens_per_seq: int, max_seq_len: int,
@@ -265,6 +269,22 @@ class StepBuffers:
                                  t, config.hidden_size, dtype=torch.float32, device=device),
             max_tokens=t, max_seq_len=max_seq_len, max_batch=max_batch,
         )
+
+    def enable_plan(self, config: LanguageConfig, tokens_per_seq: int) -> None:
+        """Run the attention launches on a per-step context-piece plan from now on (allocates the plan's
+        room once: call before any graph capture)."""
+        if self.attn_plan is None:
+            self.attn_plan = _plan_buffer(config, self.max_batch, tokens_per_seq, self.max_seq_len,
+                                          self.residual.device)
+        self.balanced = True
+
+
+def _plan_buffer(config: LanguageConfig, max_batch: int, tokens_per_seq: int, max_seq_len: int,
+                 device) -> torch.Tensor | None:
+    """Room for the attention plan of any batch up to ``max_batch`` (None if none ever splits)."""
+    n = max((attention.plan_ints(b, tokens_per_seq, config.num_heads, config.num_kv_heads, max_seq_len)
+             for b in range(1, max_batch + 1)), default=0)
+    return torch.zeros(n, dtype=torch.int32, device=device) if n else None
 
 
 class LanguageModel:
@@ -349,6 +369,10 @@ class LanguageModel:
         attn, act = buffers.attn.view_rows(t), buffers.act.view_rows(t)
         max_seq_len = min(buffers.max_seq_len, batch.block_table.shape[1] * cache.block_size)
         eps = float(c.rms_norm_eps)
+        plan = None
+        if buffers.balanced and buffers.attn_plan is not None:
+            plan = attention.build_plan(batch.seq_lens, s, c.num_heads, c.num_kv_heads, max_seq_len,
+                                        out=buffers.attn_plan)
         for index in range(start, stop):
             layer = w.layers[index]
             if not (first_norm_done and index == start):
@@ -358,7 +382,7 @@ class LanguageModel:
             attention.qk_norm_rope_paged_extend(
                 qkv, layer.q_norm, layer.k_norm, w.rope_cos, w.rope_sin, batch.positions, eps, k_cache, v_cache,
                 batch.slots, batch.seq_lens, batch.block_table, c.num_heads, scale=c.head_dim ** -0.5,
-                max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace,
+                max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace, plan=plan,
             )
             buffers.pending_splits = gemm.linear_partial(attn, layer.o, buffers.partials)
             self._settle_norm(buffers, t, layer.post_norm, stream)

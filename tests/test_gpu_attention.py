@@ -26,7 +26,7 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def _run(seq_lens, S, H, KV, block_size, num_blocks, seed, table_width=None, max_seq_len=None):
+def _run(seq_lens, S, H, KV, block_size, num_blocks, seed, table_width=None, max_seq_len=None, planned=False):
     rng = np.random.default_rng(seed)
     B = len(seq_lens)
     seq_lens = np.asarray(seq_lens, dtype=np.int32)
@@ -43,7 +43,12 @@ def _run(seq_lens, S, H, KV, block_size, num_blocks, seed, table_width=None, max
     vc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
     q = torch.randn(B, S, H, 128, generator=g, device="cuda").to(torch.bfloat16)
     table_t = torch.from_numpy(table).cuda()
-    out = attention.paged_extend(q, kc, vc, torch.from_numpy(seq_lens).cuda(), table_t, max_seq_len=max_seq_len)
+    lens_t = torch.from_numpy(seq_lens).cuda()
+    plan = None
+    if planned:
+        mx = max_seq_len or width * block_size
+        plan = attention.build_plan(lens_t, S, H, KV, mx)
+    out = attention.paged_extend(q, kc, vc, lens_t, table_t, max_seq_len=max_seq_len, plan=plan)
     torch.cuda.synchronize()
     k_rows, v_rows = [], []
     for b in range(B):
@@ -72,13 +77,69 @@ def test_ragged_contexts(seq_lens) -> None:
     _run(seq_lens, 4, 16, 8, 16, 4096, seed=32)
 
 
+@pytest.mark.parametrize("planned", [False, True])
 @pytest.mark.parametrize("seq_lens", [[5, 33, 16000, 700, 4096, 12000, 64, 2048], [16000, 40], [20000]])
-def test_widely_mixed_contexts(seq_lens) -> None:
-    """Contexts of very different lengths in one launch (each cut into the launch's split count):
-    contexts that fit one split, stored directly, beside others that are merged; a batch of two with
-    32 splits each; and one 20,000-key context over 64 splits."""
-    announce("attention mixed contexts", seq_lens)
-    _run(seq_lens, 4, 16, 8, 16, 4096, seed=37)
+def test_widely_mixed_contexts(seq_lens, planned) -> None:
+    """Contexts of very different lengths in one launch, cut into the launch's split count or by a
+    plan (long contexts taking the workgroups short ones leave): contexts of one piece, stored
+    directly, beside others that are merged; a batch of two with 32 splits each; and one 20,000-key
+    context over 64 splits."""
+    announce("attention mixed contexts", seq_lens, "planned" if planned else "even")
+    _run(seq_lens, 4, 16, 8, 16, 4096, seed=37, planned=planned)
+
+
+def test_config3_planned() -> None:
+    rng = np.random.default_rng(30)
+    seq_lens = rng.integers(2048, 8193, size=8)
+    announce("attention config3 planned", seq_lens.tolist())
+    _run(seq_lens, 4, 16, 8, 16, 65_536, seed=31, planned=True)
+
+
+@pytest.mark.parametrize("seq_lens,S,H,KV", [
+    ([5, 33, 16000, 700, 4096, 12000, 64, 2048], 4, 16, 8),
+    ([7800, 3218, 5262, 4413, 7985, 5358, 3562, 2106], 4, 16, 8),
+    ([4100] * 8, 4, 16, 8),
+    ([100, 30000, 1, 0, 2500, 9999, 17, 4096, 300, 12, 8000, 64, 640, 4097, 33, 1024], 4, 16, 8),
+    ([3000, 20], 1, 8, 8),
+])
+def test_plan_covers_every_piece_once(seq_lens, S, H, KV) -> None:
+    """The device-built plan, read back: each context's pieces 0 .. n-1 are taken by exactly one
+    workgroup slot (its own first `splits` slots, then spare slots of other sequences), no slot takes
+    two, n is at most 2 x splits, the piece table names each piece's slot, and equal contexts give
+    the even split."""
+    lens = torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
+    B = len(seq_lens)
+    max_len = max(seq_lens) + 64
+    announce("attention plan", seq_lens)
+    plan = attention.build_plan(lens, S, H, KV, max_len)
+    torch.cuda.synchronize()
+    assert plan is not None
+    p = plan.cpu().numpy()
+    splits = int(p[1])
+    assert p[0] == 1 and splits > 1 and p.size == 2 + B + 3 * B * splits
+    pieces = p[2 : 2 + B]
+    slots = p[2 + B : 2 + B + B * splits].reshape(B, splits)
+    piece_slots = p[2 + B + B * splits :].reshape(B, 2 * splits)
+    assert (pieces >= 1).all() and (pieces <= 2 * splits).all()
+    taken = {}
+    for z in range(B):
+        for x in range(splits):
+            e = int(slots[z, x])
+            if e < 0:
+                continue
+            b, j = e >> 8, e & 255
+            assert (b, j) not in taken, f"piece {(b, j)} taken twice"
+            taken[(b, j)] = (z, x)
+            if x < pieces[z]:
+                assert (b, j) == (z, x)
+    assert set(taken) == {(b, j) for b in range(B) for j in range(int(pieces[b]))}
+    for b in range(B):  # the merge's view: the slot that holds each piece, -1 past the pieces
+        for j in range(2 * splits):
+            want = (taken[(b, j)][0] << 8) | taken[(b, j)][1] if j < pieces[b] else -1
+            assert piece_slots[b, j] == want, (b, j)
+    assert int(pieces.sum()) <= B * splits
+    if len(set(seq_lens)) == 1:
+        assert (pieces == splits).all() or (pieces == pieces[0]).all()
 
 
 def test_reference_block_size_256_and_table_slack() -> None:

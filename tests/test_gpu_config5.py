@@ -8,7 +8,8 @@ head_dim 128, SwiGLU 6144, vocab 151,936, bf16, random init), block size 16.
   same layer from the same input, and pages the batch does not own left untouched.
 - The device-resident :class:`VerifyLoop` (drafting, 28-layer forward, LM head + argmax,
   acceptance, rollback in one graph) at B = 1, 4, 8, 16 and contexts 4k, 16k and uniform
-  1k-16k, two replays each against ``oracle.decoder.verify_step`` from the same state:
+  1k-16k (B = 4 and 8; at B = 8 the attention runs on a per-step piece plan), two replays each
+  against ``oracle.decoder.verify_step`` from the same state:
   * drafts bit-exact;
   * the step's LM head: its bf16 logits within one bf16 rounding of the exact product of the
     step's own final hidden states with the weight, and its greedy ids exactly the argmax of
@@ -179,13 +180,15 @@ def _exact_head_check(hidden: torch.Tensor, weight: torch.Tensor, got_logits: to
 
 
 @pytest.mark.parametrize("B,ctx", [(8, (4096, 4096)), (1, (4096, 4096)), (16, (4096, 4096)), (1, (16384, 16384)),
-                                   (4, (1024, 16384))])
+                                   (4, (1024, 16384)), (8, (1024, 16384))])
 def test_verify_loop_full_size(model, B, ctx) -> None:
     m, cpu_w = model
     steps = 2
     loop, cache, table, histories, seq_lens = _loop_case(m, B, ctx, seed=300 + B + ctx[0], steps=steps)
     S, k = loop.tokens_per_seq, loop.k
-    announce("config 5 verify loop", B, ctx)
+    # Mixed contexts at B >= 8 (here 4.3x apart) run the attention on a per-step piece plan.
+    assert loop.buffers.balanced == (ctx[0] != ctx[1] and B >= decode_graph.BALANCE_MIN_BATCH)
+    announce("config 5 verify loop", B, ctx, "planned" if loop.buffers.balanced else "even")
     loop.capture()
     hist = [list(map(int, h)) for h in histories]
     lens = [int(x) for x in seq_lens]

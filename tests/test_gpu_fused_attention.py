@@ -21,7 +21,7 @@ gemm = pkg("gemm")
 _lib = pkg("_lib")
 
 
-def _case(seq_lens, S, H, KV, block_size, seed, bad_slot=False):
+def _case(seq_lens, S, H, KV, block_size, seed, bad_slot=False, planned=False):
     rng = np.random.default_rng(seed)
     B = len(seq_lens)
     seq_lens = np.asarray(seq_lens, dtype=np.int32)
@@ -59,15 +59,17 @@ def _case(seq_lens, S, H, KV, block_size, seed, bad_slot=False):
     _lib.call("oxr_qk_norm_rope_store_at", qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(),
               sin.data_ptr(), rows, pos_t.data_ptr(), eps, k1.data_ptr(), v1.data_ptr(), slots_t.data_ptr(),
               num_blocks * block_size, B * S, H, KV, 128, q.data_ptr(), None, None, _lib.stream(torch.device(dev)))
-    out1 = attention.paged_extend(q, k1, v1, seq_t, table_t)
+    plan = attention.build_plan(seq_t, S, H, KV, table_t.shape[1] * block_size) if planned else None
+    out1 = attention.paged_extend(q, k1, v1, seq_t, table_t, plan=plan)
 
     # Fused.
     k2, v2 = kc.clone(), vc.clone()
-    out2 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k2, v2, slots_t, seq_t, table_t, H)
+    out2 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k2, v2, slots_t, seq_t, table_t, H,
+                                               plan=plan)
     # Fused, output packed for the o_proj GEMM: the same values.
     k3, v3 = kc.clone(), vc.clone()
     out3 = attention.qk_norm_rope_paged_extend(qkv, qw, kw, cos, sin, pos_t, eps, k3, v3, slots_t, seq_t, table_t, H,
-                                               out=gemm.packed_rows(B * S, H * 128, dev))
+                                               out=gemm.packed_rows(B * S, H * 128, dev), plan=plan)
     torch.cuda.synchronize()
     assert torch.equal(out2.view(torch.int16).view(B * S, H * 128), out3.unpack().view(torch.int16)), "packed output"
     assert torch.equal(k2.view(torch.int16), k3.view(torch.int16)) and torch.equal(v2.view(torch.int16), v3.view(torch.int16))
@@ -92,6 +94,16 @@ def test_verify_step_shape_and_ragged() -> None:
     lens = [4100, 4096 + 5, 2051, 8192, 300, 4127, 4128, 4129]
     announce(f"fused attention verify shape lens={lens}")
     _case(lens, 4, 16, 8, 16, seed=11)
+
+
+@pytest.mark.parametrize("S", [4, 9])
+def test_planned_mixed_contexts(S) -> None:
+    """With a plan (long contexts taking the workgroups short ones leave, so a new token's K/V row may
+    be stored by a workgroup of another sequence's slot), the fused launch still equals the separate
+    calls bit for bit, and every new row is stored exactly once."""
+    lens = [S, 40, 9000, 300, 4100, 7000, 65, 2051]
+    announce(f"fused attention planned S={S} lens={lens}")
+    _case(lens, S, 16, 8, 16, seed=30 + S, planned=True)
 
 
 def test_block_256_and_skipped_slot() -> None:
