@@ -254,7 +254,10 @@ int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight,
  * take the plan written for the same seq_lens, batch, tokens_per_seq, heads
  * and max_seq_len: every context is cut into pieces of about the batch's mean
  * share, long contexts taking the workgroups short ones leave spare (each
- * workgroup keeps its partials in its own slot of the same workspace).  Same
+ * workgroup keeps its partials in its own slot of the same workspace).  The
+ * planned calls take the plan's length (plan_ints) and refuse a shorter one;
+ * a plan written for other lengths gives wrong outputs but no access outside
+ * the launch's arrays.  Same
  * arguments, requirements and workspace as (3) and (3b) otherwise; outputs
  * within the same tolerance (the pieces differ, so the fp32 merge order does),
  * and the planned (3b) is bit-identical to the planned (3).
@@ -268,7 +271,8 @@ int oxr_paged_extend_planned(const oxr_bf16* q, const oxr_bf16* k_cache, const o
                              const int32_t* seq_lens, const int32_t* block_table, int64_t table_stride, int32_t batch,
                              int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
-                             void* workspace, size_t workspace_bytes, const int32_t* plan, oxr_stream_t stream);
+                             void* workspace, size_t workspace_bytes, const int32_t* plan, size_t plan_ints,
+                             oxr_stream_t stream);
 int oxr_qk_norm_rope_paged_extend_planned(const oxr_bf16* qkv, const oxr_bf16* q_weight, const oxr_bf16* k_weight,
                                           const oxr_bf16* cos_table, const oxr_bf16* sin_table, int64_t table_rows,
                                           const int64_t* positions, float eps, oxr_bf16* k_cache, oxr_bf16* v_cache,
@@ -278,7 +282,7 @@ int oxr_qk_norm_rope_paged_extend_planned(const oxr_bf16* qkv, const oxr_bf16* q
                                           int32_t head_dim, int32_t block_size, int64_t num_blocks,
                                           int32_t max_seq_len, float scale, oxr_bf16* out, int32_t out_packed,
                                           void* workspace, size_t workspace_bytes, const int32_t* plan,
-                                          oxr_stream_t stream);
+                                          size_t plan_ints, oxr_stream_t stream);
 
 /*
  * (3b') (3b) without a workspace argument, allocating nothing.  No counterpart

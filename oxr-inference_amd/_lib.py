@@ -48,12 +48,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_paged_extend_plan": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P]),
     "oxr_paged_extend_planned": (
         ctypes.c_int,
-        [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I32, _F32, _P, _P, _SZ, _P, _P],
+        [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I32, _F32, _P, _P, _SZ, _P, _SZ, _P],
     ),
     "oxr_qk_norm_rope_paged_extend_planned": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _F32, _P, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32,
-         _I64, _I32, _F32, _P, _I32, _P, _SZ, _P, _P],
+         _I64, _I32, _F32, _P, _I32, _P, _SZ, _P, _SZ, _P],
     ),
     "oxr_static_scratch_bytes": (ctypes.c_size_t, []),
     "oxr_qk_norm_rope_paged_extend_static": (

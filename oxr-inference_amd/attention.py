@@ -89,7 +89,7 @@ def paged_extend(
         _lib.call("oxr_paged_extend", *args, _lib.stream(device))
     else:
         _check_plan(plan, b, s, h, kv, max_seq_len, device)
-        _lib.call("oxr_paged_extend_planned", *args, plan.data_ptr(), _lib.stream(device))
+        _lib.call("oxr_paged_extend_planned", *args, plan.data_ptr(), plan.numel(), _lib.stream(device))
     return out
 
 
@@ -198,5 +198,5 @@ def qk_norm_rope_paged_extend(
         _lib.call("oxr_qk_norm_rope_paged_extend", *args, _lib.stream(device))
     else:
         _check_plan(plan, b, s, num_heads, kv, max_seq_len, device)
-        _lib.call("oxr_qk_norm_rope_paged_extend_planned", *args, plan.data_ptr(), _lib.stream(device))
+        _lib.call("oxr_qk_norm_rope_paged_extend_planned", *args, plan.data_ptr(), plan.numel(), _lib.stream(device))
     return out

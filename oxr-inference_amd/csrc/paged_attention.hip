@@ -978,7 +978,10 @@ extern "C" int oxr_paged_extend_planned(const oxr_bf16* q, const oxr_bf16* k_cac
                                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                         int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
                                         void* workspace, size_t workspace_bytes, const int32_t* plan,
-                                        oxr_stream_t stream) {
+                                        size_t plan_ints, oxr_stream_t stream) {
+  OXR_RETURN_IF(!plan || plan_ints < oxr_paged_extend_plan_ints(batch, tokens_per_seq, num_heads, num_kv_heads,
+                                                                max_seq_len),
+                OXR_ERR_INVALID_ARG);
   return oxr::launch_paged_extend(q, k_cache, v_cache, seq_lens, block_table, table_stride, batch, tokens_per_seq,
                                   num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_seq_len, scale, out,
                                   0, workspace, workspace_bytes, nullptr, plan, (hipStream_t)stream);
@@ -990,9 +993,13 @@ extern "C" int oxr_qk_norm_rope_paged_extend_planned(
     oxr_bf16* v_cache, const int64_t* slots, int64_t num_slots, const int32_t* seq_lens, const int32_t* block_table,
     int64_t table_stride, int32_t batch, int32_t tokens_per_seq, int32_t num_heads, int32_t num_kv_heads,
     int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_seq_len, float scale, oxr_bf16* out,
-    int32_t out_packed, void* workspace, size_t workspace_bytes, const int32_t* plan, oxr_stream_t stream) {
+    int32_t out_packed, void* workspace, size_t workspace_bytes, const int32_t* plan, size_t plan_ints,
+    oxr_stream_t stream) {
   using namespace oxr;
   OXR_RETURN_IF(num_slots < 0, OXR_ERR_INVALID_ARG);
+  OXR_RETURN_IF(!plan || plan_ints < oxr_paged_extend_plan_ints(batch, tokens_per_seq, num_heads, num_kv_heads,
+                                                                max_seq_len),
+                OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
                     (tokens_per_seq > kMaxNew || tokens_per_seq * (num_heads / num_kv_heads + 2) > 2 * kJobSlots),
                 OXR_ERR_UNSUPPORTED);

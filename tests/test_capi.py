@@ -113,3 +113,21 @@ def test_build_rejects_kernels_with_scratch() -> None:
         "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 56 [-Rpass-analysis=kernel-resource-usage]\n"
     )
     assert build.scratch_users(remarks) == [("k_spills", 56)]
+
+
+def test_attention_plan_sizes_and_short_plans_refused() -> None:
+    """Host side of the context-piece plans (no GPU call): a plan exists exactly when the launch
+    splits its contexts (2 + B + 3 * B * splits entries, B = 8 at 16/8 heads: 8 splits), and the
+    planned launches refuse a missing or shorter plan before launching anything."""
+    lib = pkg("_lib").lib()
+    assert lib.oxr_paged_extend_plan_ints(8, 4, 16, 8, 4112) == 2 + 8 + 3 * 8 * 8
+    assert lib.oxr_paged_extend_plan_ints(512, 4, 16, 8, 4112) == 0  # 2048 units: one piece each
+    assert lib.oxr_paged_extend_plan_ints(0, 4, 16, 8, 4112) == 0
+    need = lib.oxr_paged_extend_plan_ints(8, 4, 16, 8, 4112)
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks come first
+    args = (p, p, p, p, p, 257, 8, 4, 16, 8, 128, 16, 65536, 4112, 0.088, p, p, 1 << 30)
+    assert lib.oxr_paged_extend_planned(*args, None, need, None) == -1
+    assert lib.oxr_paged_extend_planned(*args, p, need - 1, None) == -1
+    fused = (p, p, p, p, p, 4200, p, 1e-6, p, p, p, 1 << 20, p, p, 257, 8, 4, 16, 8, 128, 16, 65536, 4112, 0.088, p,
+             0, p, 1 << 30)
+    assert lib.oxr_qk_norm_rope_paged_extend_planned(*fused, p, need - 1, None) == -1
