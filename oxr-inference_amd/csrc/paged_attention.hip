@@ -697,13 +697,12 @@ constexpr int kPlanThreads = 256;
 __global__ __launch_bounds__(kPlanThreads) void paged_extend_plan_kernel(const int32_t* __restrict__ seq_lens,
                                                                          int batch, int max_seq_len, int splits,
                                                                          int32_t* __restrict__ plan) {
-  __shared__ int s_len[kPlanMaxBatch], s_n[kPlanMaxBatch];
+  __shared__ int s_n[kPlanMaxBatch];
   __shared__ int s_spare[kPlanMaxBatch + 1], s_over[kPlanMaxBatch + 1];  // exclusive prefix sums
   __shared__ unsigned long long s_total;
   __shared__ int s_count;
   const int t = threadIdx.x;
   const int len = t < batch ? max(0, min(seq_lens[t], max_seq_len)) : 0;
-  if (t < batch) s_len[t] = len;
   if (t == 0) s_total = 0ull;
   __syncthreads();
   if (len > 0) atomicAdd(&s_total, (unsigned long long)len);
