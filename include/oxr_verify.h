@@ -423,6 +423,23 @@ int oxr_lm_head_argmax_packed(const oxr_bf16* hidden, int64_t m, const oxr_bf16*
                               int64_t vocab, oxr_bf16* logits, int64_t* predicted, void* workspace,
                               size_t workspace_bytes, oxr_stream_t stream);
 
+/*
+ * LM head + greedy argmax + acceptance in two launches: oxr_lm_head_argmax_packed followed by
+ * oxr_accept, with the argmax's cross-workgroup reduction done by the acceptance launch.
+ * Replaces LanguageModel.logits + argmax (language.py:213-214, decode_graph.py:167) and
+ * speculative.accept with the engine's rollback (speculative.py:42-48, engine.py:729-737).
+ * m = batch * tokens_per_seq token rows (at most 256; tokens_per_seq at most 256), sequence b's
+ * rows b * tokens_per_seq .. + tokens_per_seq - 1.  predicted (int64 [m]) receives the greedy
+ * ids; every other argument and output is that of oxr_lm_head_argmax_packed (logits are not
+ * written) or oxr_accept, with the same results bit for bit.
+ */
+int oxr_lm_head_accept_packed(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight_packed, int64_t hidden_size,
+                              int64_t vocab, void* workspace, size_t workspace_bytes, int64_t* predicted,
+                              const int32_t* draft, const int32_t* draft_len, int32_t k, int32_t tokens_per_seq,
+                              int32_t batch, int32_t eos_id, const int32_t* max_tokens, int32_t* accepted,
+                              int32_t* committed, int32_t* num_committed, int32_t* seq_len, int32_t* history,
+                              int64_t history_stride, int32_t* history_len, int32_t* finished, oxr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_gemm_bf16_partial": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P]),
     "oxr_lm_head_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "oxr_lm_head_argmax": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "oxr_lm_head_accept_packed": (
+        ctypes.c_int,
+        [_P, _I64, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I64, _P, _P,
+         _P],
+    ),
     "oxr_argmax_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "oxr_argmax": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "oxr_varlen_attention": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P]),

@@ -44,6 +44,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "lm_head_keys.h"
 
 namespace oxr {
 namespace {
@@ -1019,20 +1020,19 @@ int gemm_partial_entry(const oxr_bf16* x, int64_t ldx, int64_t m, const oxr_bf16
   return OXR_OK;
 }
 
-int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
-                  oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes, bool packed,
-                  oxr_stream_t stream) {
+int lm_head_keys_impl(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
+                      oxr_bf16* logits, void* workspace, size_t workspace_bytes, bool packed, hipStream_t s,
+                      const uint64_t** best_out, int* num_best_out) {
+  *num_best_out = 0;
   // More than 64 rows only on the wide path (packed weight, up to 256 rows); the common checks see at most 64.
   OXR_RETURN_IF(m > 64 && !lm_head_wide_supported(m, hidden_size, packed), OXR_ERR_UNSUPPORTED);
   int st = check_common(hidden, hidden_size, std::min<int64_t>(m, 64), weight, hidden_size, vocab);
   if (st) return st;
-  OXR_RETURN_IF(!predicted, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(logits && (uintptr_t)logits % 8 != 0, OXR_ERR_UNSUPPORTED);
   OXR_RETURN_IF(vocab > 0x7fffffffLL, OXR_ERR_UNSUPPORTED);
   if (m == 0) return OXR_OK;
   const size_t need = oxr_lm_head_workspace_bytes(m, vocab);
   OXR_RETURN_IF(!workspace || workspace_bytes < need, OXR_ERR_WORKSPACE);
-  hipStream_t s = (hipStream_t)stream;
   uint64_t* best = static_cast<uint64_t*>(workspace);
   int num_best;  // partial maxima per token for the final reduction
   if (lm_head_wide_supported(m, hidden_size, packed)) {
@@ -1064,12 +1064,37 @@ int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int
     st = dispatch<kArgmax>(a, c, packed ? kPackedW : kRowMajor, s);
   }
   if (st) return st;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint64_t*>(best),
-                     num_best, (int)m, predicted);
+  *best_out = best;
+  *num_best_out = num_best;
+  return OXR_OK;
+}
+
+int lm_head_entry(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
+                  oxr_bf16* logits, int64_t* predicted, void* workspace, size_t workspace_bytes, bool packed,
+                  oxr_stream_t stream) {
+  hipStream_t s = (hipStream_t)stream;
+  // Checked in the order of the key launch's own checks, with predicted after the operands.
+  OXR_RETURN_IF(m > 64 && !lm_head_wide_supported(m, hidden_size, packed), OXR_ERR_UNSUPPORTED);
+  const int common = check_common(hidden, hidden_size, std::min<int64_t>(m, 64), weight, hidden_size, vocab);
+  if (common) return common;
+  OXR_RETURN_IF(!predicted, OXR_ERR_INVALID_ARG);
+  const uint64_t* best = nullptr;
+  int num_best = 0;
+  const int st = lm_head_keys_impl(hidden, m, weight, hidden_size, vocab, logits, workspace, workspace_bytes, packed,
+                                   s, &best, &num_best);
+  if (st || m == 0) return st;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3((unsigned)m), dim3(256), 0, s, best, num_best, (int)m, predicted);
   return OXR_LAUNCH_STATUS();
 }
 
 }  // namespace
+
+int lm_head_keys(const oxr_bf16* hidden, int64_t m, const oxr_bf16* weight, int64_t hidden_size, int64_t vocab,
+                 oxr_bf16* logits, void* workspace, size_t workspace_bytes, bool packed, hipStream_t stream,
+                 const uint64_t** best, int* num_best) {
+  return lm_head_keys_impl(hidden, m, weight, hidden_size, vocab, logits, workspace, workspace_bytes, packed, stream,
+                           best, num_best);
+}
 }  // namespace oxr
 
 extern "C" size_t oxr_packed_weight_elems(int64_t rows, int64_t k) {

@@ -339,12 +339,18 @@ class VerifyLoop:
         batch = ExtendBatch(inp.ids, inp.positions, inp.slots, inp.attn_seq_lens, self.block_table,
                             self.tokens_per_seq)
         hidden = self.language.extend(batch, self.cache, self.buffers)
-        predicted = self.language.greedy(hidden, self.buffers)
-        speculative.accept_batch(
-            inp.draft, inp.draft_len, predicted.view(self.batch, self.tokens_per_seq), seq_len=self.seq_len,
-            history=self.history, history_len=self.history_len, eos_id=self.eos_id, max_tokens=self.max_tokens,
-            finished=self.finished, out=self.accepted,
-        )
+        state = dict(seq_len=self.seq_len, history=self.history, history_len=self.history_len, eos_id=self.eos_id,
+                     max_tokens=self.max_tokens, finished=self.finished, out=self.accepted)
+        head = self.language.weights.lm_head
+        if isinstance(head, gemm.PackedWeight):  # the argmax finished inside the acceptance launch
+            predicted = self.buffers.predicted[: self.batch * self.tokens_per_seq]
+            speculative.greedy_accept_batch(hidden, head, inp.draft, inp.draft_len,
+                                            predicted=predicted.view(self.batch, self.tokens_per_seq),
+                                            workspace=self.buffers.head_workspace, **state)
+        else:
+            predicted = self.language.greedy(hidden, self.buffers)
+            speculative.accept_batch(inp.draft, inp.draft_len, predicted.view(self.batch, self.tokens_per_seq),
+                                     **state)
 
     def capture(self, stream: torch.cuda.Stream | None = None) -> None:
         """One eager step on the capture stream (state restored afterwards), then the step captured."""

@@ -9,6 +9,8 @@ as gfx950 kernels over device-resident histories:
   engine.py:700-710 (ids, positions, slots, seq_lens), so the step needs no host data.
 - ``accept_batch``: longest-prefix acceptance, length rollback and history append for
   all sequences in one launch (csrc/accept.hip).
+- ``greedy_accept_batch``: the LM head's greedy ids and ``accept_batch`` on them, with the
+  argmax finished inside the acceptance launch.
 
 ``NgramProposer`` and ``accept`` keep the reference's list-based signatures for callers
 that hold Python lists; they run the same kernels on a batch of one.
@@ -22,6 +24,7 @@ from typing import NamedTuple
 import torch
 
 from . import _lib
+from .gemm import PackedWeight
 
 _MAX_N = 4  # speculative.py:12
 
@@ -125,22 +128,11 @@ class AcceptResult(NamedTuple):
     num_committed: torch.Tensor  # int32 [B]: a + 1
 
 
-def accept_batch(
-    draft: torch.Tensor, draft_len: torch.Tensor, predicted: torch.Tensor, *, seq_len: torch.Tensor | None = None,
-    history: torch.Tensor | None = None, history_len: torch.Tensor | None = None, eos_id: int = -1,
-    max_tokens: torch.Tensor | None = None, finished: torch.Tensor | None = None, out: AcceptResult | None = None,
-) -> AcceptResult:
-    """speculative.accept for every sequence plus the engine's rollback (engine.py:729-737):
-    ``seq_len += a + 1`` and the committed ids appended to ``history`` (stopping at ``eos_id`` or
-    ``max_tokens``, reported in ``finished``).  ``predicted`` is the step's int64 ``[B, S]`` greedy ids."""
-    device = _lib.require_gpu(draft, draft_len, predicted, seq_len, history, history_len, max_tokens, finished,
-                              name="accept_batch")
+def _accept_args(draft, draft_len, s, seq_len, history, history_len, max_tokens, finished, out, device):
+    """Checks shared by the acceptance entry points; the output tensors (``out`` or new ones)."""
     _check_int32("draft", draft, 2)
     _check_int32("draft_len", draft_len, 1)
     b, k = draft.shape
-    _lib.require(predicted.dtype == torch.int64 and predicted.dim() == 2 and predicted.shape[0] == b
-                 and predicted.is_contiguous(), "predicted must be contiguous int64 [B, S]")
-    s = predicted.shape[1]
     for name, t in (("seq_len", seq_len), ("history_len", history_len), ("max_tokens", max_tokens),
                     ("finished", finished)):
         if t is not None:
@@ -153,11 +145,63 @@ def accept_batch(
         out = AcceptResult(torch.empty(b, dtype=torch.int32, device=device),
                            torch.empty(b, k + 1, dtype=torch.int32, device=device),
                            torch.empty(b, dtype=torch.int32, device=device))
+    return out
+
+
+def accept_batch(
+    draft: torch.Tensor, draft_len: torch.Tensor, predicted: torch.Tensor, *, seq_len: torch.Tensor | None = None,
+    history: torch.Tensor | None = None, history_len: torch.Tensor | None = None, eos_id: int = -1,
+    max_tokens: torch.Tensor | None = None, finished: torch.Tensor | None = None, out: AcceptResult | None = None,
+) -> AcceptResult:
+    """speculative.accept for every sequence plus the engine's rollback (engine.py:729-737):
+    ``seq_len += a + 1`` and the committed ids appended to ``history`` (stopping at ``eos_id`` or
+    ``max_tokens``, reported in ``finished``).  ``predicted`` is the step's int64 ``[B, S]`` greedy ids."""
+    device = _lib.require_gpu(draft, draft_len, predicted, seq_len, history, history_len, max_tokens, finished,
+                              name="accept_batch")
+    b, k = draft.shape
+    _lib.require(predicted.dtype == torch.int64 and predicted.dim() == 2 and predicted.shape[0] == b
+                 and predicted.is_contiguous(), "predicted must be contiguous int64 [B, S]")
+    s = predicted.shape[1]
+    out = _accept_args(draft, draft_len, s, seq_len, history, history_len, max_tokens, finished, out, device)
     _lib.call(
         "oxr_accept", draft.data_ptr(), draft_len.data_ptr(), k, predicted.data_ptr(), s, b, int(eos_id),
         _lib.ptr(max_tokens), out.accepted.data_ptr(), out.committed.data_ptr(), out.num_committed.data_ptr(),
         _lib.ptr(seq_len), _lib.ptr(history), history.stride(0) if history is not None else 0, _lib.ptr(history_len),
         _lib.ptr(finished), _lib.stream(device),
+    )
+    return out
+
+
+def greedy_accept_batch(
+    hidden: torch.Tensor, lm_head: PackedWeight, draft: torch.Tensor, draft_len: torch.Tensor, *,
+    predicted: torch.Tensor, workspace: torch.Tensor, seq_len: torch.Tensor | None = None,
+    history: torch.Tensor | None = None, history_len: torch.Tensor | None = None, eos_id: int = -1,
+    max_tokens: torch.Tensor | None = None, finished: torch.Tensor | None = None, out: AcceptResult | None = None,
+) -> AcceptResult:
+    """The verify step's tail in two launches (``oxr_lm_head_accept_packed``): the greedy ids of
+    ``hidden`` (bf16 ``[B * S, hidden]``) under the packed LM head into ``predicted`` (int64
+    ``[B, S]``; language.py:213-214, decode_graph.py:167), then :func:`accept_batch` on them, with
+    the argmax's last reduction done by the acceptance launch.  Same results as
+    ``lm_head.lm_head_argmax`` followed by :func:`accept_batch`.  ``workspace``: at least
+    ``lm_head.workspace_bytes(B * S, vocab)`` bytes."""
+    device = _lib.require_gpu(hidden, lm_head.data, draft, draft_len, predicted, workspace, seq_len, history,
+                              history_len, max_tokens, finished, name="greedy_accept_batch")
+    b, k = draft.shape
+    _lib.require(predicted.dtype == torch.int64 and predicted.dim() == 2 and predicted.shape[0] == b
+                 and predicted.is_contiguous(), "predicted must be contiguous int64 [B, S]")
+    s = predicted.shape[1]
+    _lib.require(hidden.dtype == torch.bfloat16 and hidden.dim() == 2 and hidden.shape[0] == b * s
+                 and hidden.stride(1) == 1 and hidden.shape[1] == lm_head.shape[1],
+                 "hidden must be bf16 [B * S, hidden] with contiguous rows")
+    _lib.require(hidden.stride(0) == hidden.shape[1], "hidden rows must be packed back to back")
+    out = _accept_args(draft, draft_len, s, seq_len, history, history_len, max_tokens, finished, out, device)
+    _lib.call(
+        "oxr_lm_head_accept_packed", hidden.data_ptr(), b * s, lm_head.data.data_ptr(), hidden.shape[1],
+        lm_head.shape[0], workspace.data_ptr(), workspace.numel() * workspace.element_size(), predicted.data_ptr(),
+        draft.data_ptr(), draft_len.data_ptr(), k, s, b, int(eos_id), _lib.ptr(max_tokens), out.accepted.data_ptr(),
+        out.committed.data_ptr(), out.num_committed.data_ptr(), _lib.ptr(seq_len), _lib.ptr(history),
+        history.stride(0) if history is not None else 0, _lib.ptr(history_len), _lib.ptr(finished),
+        _lib.stream(device),
     )
     return out
 

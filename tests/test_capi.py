@@ -131,3 +131,25 @@ def test_attention_plan_sizes_and_short_plans_refused() -> None:
     fused = (p, p, p, p, p, 4200, p, 1e-6, p, p, p, 1 << 20, p, p, 257, 8, 4, 16, 8, 128, 16, 65536, 4112, 0.088, p,
              0, p, 1 << 30)
     assert lib.oxr_qk_norm_rope_paged_extend_planned(*fused, p, need - 1, None) == -1
+
+
+def test_lm_head_accept_refusals() -> None:
+    """Host checks of oxr_lm_head_accept_packed (no GPU call): the token rows must be exactly
+    batch * tokens_per_seq, at most 256 of them and at most 256 per sequence; acceptance arguments
+    are checked as oxr_accept checks them; a batch of 0 launches nothing."""
+    lib = pkg("_lib").lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks come first
+
+    def call(m, k, s, batch, predicted=p, draft_len=p, history=None, history_len=None):
+        return lib.oxr_lm_head_accept_packed(p, m, p, 2048, 151936, p, 1 << 30, predicted, p, draft_len, k, s,
+                                             batch, -1, None, p, None, None, None, history, 0, history_len, None,
+                                             None)
+
+    assert call(33, 3, 4, 8) == -1     # m != batch * tokens_per_seq
+    assert call(32, 3, 4, 8, predicted=None) == -1
+    assert call(32, 3, 4, 8, draft_len=None) == -1
+    assert call(32, 3, 4, 8, history=p) == -1  # history without history_len
+    assert call(32, -1, 4, 8) == -1
+    assert call(260, 3, 4, 65) == -2   # more than 256 rows
+    assert call(257, 256, 257, 1) == -2  # more than 256 rows per sequence
+    assert call(0, 3, 4, 0) == 0

@@ -284,3 +284,63 @@ def test_argmax_edge_cases(dtype) -> None:
     assert np.array_equal(lm_head.argmax(strided).cpu().numpy(), a[:, 1:1001].float().argmax(-1).numpy())
     batch = a[:8].reshape(2, 4, vocab)  # leading dims kept
     assert lm_head.argmax(batch.cuda()).shape == (2, 4)
+
+
+gemm = pkg("gemm")
+
+
+@pytest.mark.parametrize("B,S,vocab", [(8, 4, 151936), (1, 4, 32768), (8, 9, 32768), (16, 4, 32768),
+                                       (12, 20, 32768), (64, 4, 5000)])
+def test_greedy_accept_matches_separate_launches(B: int, S: int, vocab: int) -> None:
+    """oxr_lm_head_accept_packed against oxr_lm_head_argmax_packed followed by oxr_accept on the
+    same inputs: greedy ids, accepted lengths, committed ids, KV lengths, histories and finish
+    reasons bit for bit.  Rows 32 and under take the persistent LM head, more the wide one;
+    S = 20 needs two rounds of key loads.  Drafts copy the separate path's ids with p = 0.6 per
+    position, so runs of every length are accepted; the last sequence starts finished, one id is
+    the EOS and max_tokens stops some histories."""
+    rng = np.random.default_rng(100 * B + S)
+    gen = torch.Generator(device="cuda").manual_seed(B + S)
+    hidden = torch.randn(B * S, 2048, device="cuda", generator=gen).to(torch.bfloat16)
+    w = gemm.pack_weight((torch.randn(vocab, 2048, device="cuda", generator=gen) * 0.02).to(torch.bfloat16))
+    ws = torch.empty(lm_head.workspace_bytes(B * S, vocab), dtype=torch.uint8, device="cuda")
+    announce(f"greedy accept B={B} S={S} vocab={vocab}: separate launches")
+    pred_ref = lm_head.lm_head_argmax(hidden, w, workspace=ws)[0]
+    pr = pred_ref.view(B, S).cpu().numpy()
+    k = S - 1
+    draft = np.where(rng.random((B, k)) < 0.6, pr[:, :k], rng.integers(0, vocab, (B, k))).astype(np.int32)
+    dlen = rng.integers(0, k + 1, size=B).astype(np.int32)
+    dlen[0] = k
+    draft[0] = pr[0, :k]  # one full accept
+    cap = 64
+    hist_len = rng.integers(1, 30, size=B).astype(np.int32)
+    hist = rng.integers(0, vocab, size=(B, cap)).astype(np.int32)
+    max_tokens = (hist_len + rng.integers(1, S + 2, size=B)).astype(np.int32)
+    fin = np.zeros(B, dtype=np.int32)
+    if B > 1:
+        fin[-1] = 2
+    eos = int(pr[B // 2, 1])
+    seq_len = rng.integers(100, 9000, size=B).astype(np.int32)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    def state():
+        return dict(seq_len=d(seq_len), history=d(hist), history_len=d(hist_len), max_tokens=d(max_tokens),
+                    finished=d(fin), eos_id=eos)
+
+    ref = state()
+    res_ref = spec.accept_batch(d(draft), d(dlen), pred_ref.view(B, S), **ref)
+    announce(f"greedy accept B={B} S={S} vocab={vocab}: fused")
+    got = state()
+    pred = torch.full((B, S), -7, dtype=torch.int64, device="cuda")
+    ws.fill_(0xAB)
+    res = spec.greedy_accept_batch(hidden, w, d(draft), d(dlen), predicted=pred, workspace=ws, **got)
+    assert torch.equal(pred.view(-1), pred_ref)
+    for name in ("accepted", "committed", "num_committed"):
+        assert torch.equal(getattr(res, name), getattr(res_ref, name)), name
+    for name in ("seq_len", "history", "history_len", "finished"):
+        assert torch.equal(got[name], ref[name]), name
+    acc = res.accepted.cpu().numpy()
+    assert acc[0] == k
+    if B > 2:
+        assert (acc[:-1] < k).any()
+    if B > 1:
+        assert acc[-1] == 0 and res.num_committed[-1].item() == 0  # started finished
