@@ -173,31 +173,31 @@ def accept_batch(
 
 
 def greedy_accept_batch(
-    hidden: torch.Tensor, lm_head: PackedWeight, draft: torch.Tensor, draft_len: torch.Tensor, *,
+    hidden: torch.Tensor, head_weight: PackedWeight, draft: torch.Tensor, draft_len: torch.Tensor, *,
     predicted: torch.Tensor, workspace: torch.Tensor, seq_len: torch.Tensor | None = None,
     history: torch.Tensor | None = None, history_len: torch.Tensor | None = None, eos_id: int = -1,
     max_tokens: torch.Tensor | None = None, finished: torch.Tensor | None = None, out: AcceptResult | None = None,
 ) -> AcceptResult:
     """The verify step's tail in two launches (``oxr_lm_head_accept_packed``): the greedy ids of
-    ``hidden`` (bf16 ``[B * S, hidden]``) under the packed LM head into ``predicted`` (int64
+    ``hidden`` (bf16 ``[B * S, hidden]``) under the packed LM head ``head_weight`` into ``predicted`` (int64
     ``[B, S]``; language.py:213-214, decode_graph.py:167), then :func:`accept_batch` on them, with
     the argmax's last reduction done by the acceptance launch.  Same results as
     ``lm_head.lm_head_argmax`` followed by :func:`accept_batch`.  ``workspace``: at least
     ``lm_head.workspace_bytes(B * S, vocab)`` bytes."""
-    device = _lib.require_gpu(hidden, lm_head.data, draft, draft_len, predicted, workspace, seq_len, history,
+    device = _lib.require_gpu(hidden, head_weight.data, draft, draft_len, predicted, workspace, seq_len, history,
                               history_len, max_tokens, finished, name="greedy_accept_batch")
     b, k = draft.shape
     _lib.require(predicted.dtype == torch.int64 and predicted.dim() == 2 and predicted.shape[0] == b
                  and predicted.is_contiguous(), "predicted must be contiguous int64 [B, S]")
     s = predicted.shape[1]
     _lib.require(hidden.dtype == torch.bfloat16 and hidden.dim() == 2 and hidden.shape[0] == b * s
-                 and hidden.stride(1) == 1 and hidden.shape[1] == lm_head.shape[1],
+                 and hidden.stride(1) == 1 and hidden.shape[1] == head_weight.shape[1],
                  "hidden must be bf16 [B * S, hidden] with contiguous rows")
     _lib.require(hidden.stride(0) == hidden.shape[1], "hidden rows must be packed back to back")
     out = _accept_args(draft, draft_len, s, seq_len, history, history_len, max_tokens, finished, out, device)
     _lib.call(
-        "oxr_lm_head_accept_packed", hidden.data_ptr(), b * s, lm_head.data.data_ptr(), hidden.shape[1],
-        lm_head.shape[0], workspace.data_ptr(), workspace.numel() * workspace.element_size(), predicted.data_ptr(),
+        "oxr_lm_head_accept_packed", hidden.data_ptr(), b * s, head_weight.data.data_ptr(), hidden.shape[1],
+        head_weight.shape[0], workspace.data_ptr(), workspace.numel() * workspace.element_size(), predicted.data_ptr(),
         draft.data_ptr(), draft_len.data_ptr(), k, s, b, int(eos_id), _lib.ptr(max_tokens), out.accepted.data_ptr(),
         out.committed.data_ptr(), out.num_committed.data_ptr(), _lib.ptr(seq_len), _lib.ptr(history),
         history.stride(0) if history is not None else 0, _lib.ptr(history_len), _lib.ptr(finished),
