@@ -615,6 +615,13 @@ __device__ __forceinline__ void merge_planned(const float* __restrict__ part_o, 
 // Merge of the context splits of every (sequence, kv head): one workgroup per
 // pair, one thread per 4 output dims of a row.  Sequences whose context fitted
 // one split were already stored by the main kernel.
+// The merge's workgroups split each row's kD dims into 4 slices when a (sequence, kv head) has 8 or
+// more rows, 2 from 4 rows, else 1, so that every workgroup still fills a wave: at B = 8, S = 4 the
+// launch is 256 one-wave workgroups, each reading a quarter of a (sequence, kv head)'s partials.
+// Measured against one slice: verify step 2151.5 vs 2157 us; one token per sequence (2 rows) with 4
+// slices made the decode step 3 us slower, hence the row threshold.
+int merge_dim_slices(int rows) { return rows >= 8 ? 4 : rows >= 4 ? 2 : 1; }
+
 template <bool kPlanned>
 __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(const float* __restrict__ part_o,
                                                                               const float* __restrict__ part_ml,
@@ -627,8 +634,12 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
   constexpr int kChunk = 8;  // splits whose partials are requested together
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int G = H / KV;
-  // One thread per 4 output dims of a row (blockDim = rows * 32).
-  const int rr = threadIdx.x / (kD / 4), d0 = (threadIdx.x % (kD / 4)) * 4;
+  // One thread per 4 output dims of a row; with gridDim.z = 1, 2 or 4 dim slices, workgroup z takes
+  // dims [z, z + 1) * kD / gridDim.z of every row (blockDim = rows * kD / 4 / gridDim.z).
+  const int shift = __builtin_ctz(gridDim.z);
+  const int per_row = (kD / 4) >> shift;
+  const int rr = threadIdx.x / per_row;
+  const int d0 = (int)blockIdx.z * (kD >> shift) + (threadIdx.x & (per_row - 1)) * 4;
   if constexpr (kPlanned) {
     const int pieces = min(max(plan[kPlanHead + b], 1), 2 * splits);
     merge_planned(part_o, part_ml, pieces, plan + kPlanHead + (int)gridDim.y * (1 + splits) + b * 2 * splits, b,
@@ -898,8 +909,9 @@ int launch_paged_extend(const oxr_bf16* q, const oxr_bf16* k_cache, const oxr_bf
   int status = OXR_LAUNCH_STATUS();
   if (status || splits == 1) return status;
   const int rows = tokens_per_seq * (num_heads / num_kv_heads);
-  hipLaunchKernelGGL(plan ? paged_extend_merge_kernel<true> : paged_extend_merge_kernel<false>, dim3(num_kv_heads, batch),
-                     dim3(rows * kD / 4), 0, s, part_o, part_ml,
+  hipLaunchKernelGGL(plan ? paged_extend_merge_kernel<true> : paged_extend_merge_kernel<false>,
+                     dim3(num_kv_heads, batch, merge_dim_slices(rows)), dim3(rows * kD / 4 / merge_dim_slices(rows)), 0,
+                     s, part_o, part_ml,
                      seq_lens, tokens_per_seq, num_heads, num_kv_heads, max_seq_len, splits, plan, out, out_packed);
   return OXR_LAUNCH_STATUS();
 }
