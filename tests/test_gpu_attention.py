@@ -193,9 +193,11 @@ def test_reference_default_width_s9() -> None:
     _run([300, 9, 1000, 2600], 9, 16, 8, 256, 64, seed=38)
 
 
-@pytest.mark.parametrize("S,H,KV", [(16, 16, 8), (12, 8, 8), (5, 32, 8), (16, 16, 16)])
+@pytest.mark.parametrize("S,H,KV", [(16, 16, 8), (12, 8, 8), (5, 32, 8), (16, 16, 16), (2, 16, 8), (3, 16, 8),
+                                    (7, 8, 8)])
 def test_query_row_tiles(S, H, KV) -> None:
     """Up to 32 query rows per kv head: 16 tokens x 2 heads (both tiles full), 12 x 1, 5 x 4 (20
-    rows), 16 tokens of MHA; contexts shorter than S, inside one split, and across splits."""
+    rows), 16 tokens of MHA; contexts shorter than S, inside one split, and across splits.  4, 6
+    and 7 rows take the split merge in two dim slices (8 and more rows: four; fewer than 4: one)."""
     announce("attention row tiles", S, H, KV)
     _run([S, S + 1, 700, 3000], S, H, KV, 16, 1024, seed=39 + S + H)
