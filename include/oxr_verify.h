@@ -181,6 +181,16 @@ int oxr_embed_rms_norm(const int64_t* ids, int64_t rows, const oxr_bf16* table, 
                        oxr_stream_t stream);
 
 /*
+ * Embedding lookup (the reference's nn.Embedding embed_tokens, language.py:155),
+ * as the eager decode and verify paths call it before building a DecodeBatch /
+ * ExtendBatch (engine.py:595, 717; decode_graph.py:75, 164): out[i] =
+ * table[ids[i]], bf16 [rows, ldo].  Ids outside [0, vocab) are clamped (the
+ * reference callers pass ids.clamp(min=0), model.py:32).
+ */
+int oxr_embed_gather(const int64_t* ids, int64_t rows, const oxr_bf16* table, int64_t vocab, int64_t hidden,
+                     oxr_bf16* out, int64_t ldo, oxr_stream_t stream);
+
+/*
  * Residual add + RMSNorm from GEMM partials (_add_rms_norm, language.py:94-99):
  * residual = bf16(bf16(sum_s partials[s]) + residual) in place, then out =
  * rms_norm(residual) as oxr_rms_norm.  partials fp32 [k_splits, rows, hidden]
@@ -255,9 +265,14 @@ int oxr_qk_norm_rope_paged_extend(const oxr_bf16* qkv, const oxr_bf16* q_weight,
  * and max_seq_len: every context is cut into pieces of about the batch's mean
  * share, long contexts taking the workgroups short ones leave spare (each
  * workgroup keeps its partials in its own slot of the same workspace).  The
- * planned calls take the plan's length (plan_ints) and refuse a shorter one;
- * a plan written for other lengths gives wrong outputs but no access outside
- * the launch's arrays.  Same
+ * planned calls take the plan's length (plan_ints) and refuse a shorter one.
+ * The plan's header records the batch and split count it was written for; a
+ * launch whose batch or split count differs (another max_seq_len or
+ * tokens_per_seq) ignores it and runs on even pieces, bit-identical to (3) /
+ * (3b).  A plan written from other seq_lens whose pieces do not reach a
+ * context's end, or that names pieces outside the launch, makes that
+ * sequence's output rows NaN; nothing is addressed outside the launch's
+ * arrays.  Same
  * arguments, requirements and workspace as (3) and (3b) otherwise; outputs
  * within the same tolerance (the pieces differ, so the fp32 merge order does),
  * and the planned (3b) is bit-identical to the planned (3).

@@ -114,6 +114,17 @@ int launch(const bf16_t* x, int64_t ldx, const int64_t* ids, int64_t vocab, cons
   return OXR_LAUNCH_STATUS();
 }
 
+// The embedding lookup alone (nn.Embedding, language.py:155, as the eager paths call it:
+// engine.py:595, 717): out[row] = table[ids[row]], one 16-byte vector per thread.
+__global__ __launch_bounds__(kMaxThreads) void embed_gather_kernel(const int64_t* __restrict__ ids, int64_t vocab,
+                                                                   const bf16_t* __restrict__ table, int D,
+                                                                   bf16_t* __restrict__ out, int64_t ldo) {
+  int64_t id = ids[blockIdx.x];
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // stay inside the table
+  const int col = threadIdx.x * 8;
+  st128(out + (int64_t)blockIdx.x * ldo + col, ld128(table + id * D + col));
+}
+
 int check(int64_t rows, int64_t D, int64_t ld, int64_t ldo) {
   OXR_RETURN_IF(rows < 0 || D <= 0 || ld < D || ldo < D, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(D % (kWave * 8) != 0 || D > kMaxThreads * 8 || ld % 8 != 0 || ldo % 8 != 0, OXR_ERR_UNSUPPORTED);
@@ -158,4 +169,16 @@ extern "C" int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits
   OXR_RETURN_IF(!partials || !residual || !weight || !out, OXR_ERR_INVALID_ARG);
   return launch<kAddPartials>(nullptr, hidden, nullptr, 0, partials, k_splits, (int)rows, (int)hidden, weight, eps,
                               residual, out, hidden, out_packed ? 1 : 0, (hipStream_t)stream);
+}
+
+extern "C" int oxr_embed_gather(const int64_t* ids, int64_t rows, const oxr_bf16* table, int64_t vocab, int64_t hidden,
+                                oxr_bf16* out, int64_t ldo, oxr_stream_t stream) {
+  using namespace oxr;
+  int st = check(rows, hidden, hidden, ldo);
+  if (st) return st;
+  if (rows == 0) return OXR_OK;
+  OXR_RETURN_IF(!ids || !table || vocab <= 0 || !out, OXR_ERR_INVALID_ARG);
+  hipLaunchKernelGGL(embed_gather_kernel, dim3((unsigned)rows), dim3((unsigned)(hidden / 8)), 0, (hipStream_t)stream,
+                     ids, vocab, table, (int)hidden, out, ldo);
+  return OXR_LAUNCH_STATUS();
 }

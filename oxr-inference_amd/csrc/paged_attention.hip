@@ -153,7 +153,7 @@ constexpr int kMaxRowTiles = 2;      // 16-row MFMA tiles of query rows per (seq
 constexpr int kPartRows = 16 * kMaxRowTiles;  // row stride of the split partials
 constexpr int kMaxNew = 16;          // new tokens per sequence (S) of the fused kernel
 constexpr int kJobSlots = 64 * kWaves / 16;   // 16-lane row jobs per round of the fused prologue
-constexpr int kPlanHead = 2;         // plan: [valid, splits, pieces per sequence..., slot entries...]
+constexpr int kPlanHead = 2;         // plan: [batch, splits, pieces per sequence..., slot entries...]
 
 // Inputs of the fused q/k norm + RoPE + KV store (oxr_qk_norm_rope_paged_extend).
 struct RopeArgs {
@@ -198,9 +198,12 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   __shared__ int s_pages[kMaxSpanPages];
 
   // Which piece of which context this workgroup takes: piece blockIdx.x of sequence blockIdx.z of
-  // `splits` even pieces, or, with a plan (paged_extend_plan_kernel), the entry of its slot.
+  // `splits` even pieces, or, with a plan (paged_extend_plan_kernel), the entry of its slot.  A plan
+  // whose header names another batch or split count was written for another launch: the launch then
+  // runs on even pieces (the merge makes the same test), which read and write the same units.
   int split = blockIdx.x, b = blockIdx.z, pieces = 0;
-  if constexpr (kPlanned) {
+  const bool use_plan = kPlanned && plan[0] == (int)gridDim.z && plan[1] == splits;
+  if (use_plan) {
     const int a = plan[kPlanHead + gridDim.z + blockIdx.z * splits + blockIdx.x];
     // A spare slot the plan leaves idle (workgroup-uniform); entries out of range (a plan written for
     // another launch) are treated alike, so nothing is addressed outside the launch's arrays.
@@ -270,12 +273,15 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
   // This workgroup's keys: piece `split` of [0, L), in whole 32-key pairs.
   // (A plan's pieces are never longer than an even split of max_seq_len; the clamp keeps the page
   // range inside the LDS copy whatever the plan holds.)
-  const int span = kPlanned ? min(((L + pieces - 1) / pieces + 31) / 32 * 32,
+  const int span = use_plan ? min(((L + pieces - 1) / pieces + 31) / 32 * 32,
                                   ((max_seq_len + splits - 1) / splits + 31) / 32 * 32)
                             : ((L + splits - 1) / splits + 31) / 32 * 32;
   const int t_begin = split * span;
   const int t_end = min(L, t_begin + span);
-  const bool single = kPlanned ? pieces == 1 : L <= span;  // the whole context is in piece 0
+  const bool single = use_plan ? pieces == 1 : L <= span;  // the whole context is in piece 0
+  // A plan built from other (shorter) lengths can leave keys past its pieces; that sequence's rows
+  // are then written as NaN (here when it has one piece, else by the merge) instead of dropping keys.
+  const bool uncovered = use_plan && (int64_t)pieces * span < L;
   if (single && split > 0) return;
   const int32_t* table_row = block_table + (int64_t)b * table_stride;
 
@@ -537,7 +543,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
       const int rr = 16 * t + rl;
       const int kvh_o = (int)blockIdx.y * HPW + ho;
       // Even: the (sequence, piece) unit; planned: this workgroup's own slot (the plan maps pieces to slots).
-      const int64_t unit = kPlanned ? ((int64_t)blockIdx.z * KV + kvh_o) * splits + blockIdx.x
+      const int64_t unit = use_plan ? ((int64_t)blockIdx.z * KV + kvh_o) * splits + blockIdx.x
                                     : ((int64_t)b * KV + kvh_o) * splits + split;
       float mmax = -INFINITY;
 #pragma unroll
@@ -553,7 +559,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
         acc += *reinterpret_cast<const f32x4*>(&s_o[w][rl][d0]) * wt;
       }
       if (single) {
-        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        const float inv = uncovered ? __builtin_nanf("") : l > 0.f ? 1.0f / l : 0.f;
         const int s = rr / G, hh = rr % G;
         uint32_t* dst = out_vec(out, (int64_t)b * S + s, (kvh_o * G + hh) * kD + d0, H * kD, out_packed);
         dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
@@ -571,22 +577,30 @@ __global__ __launch_bounds__(64 * kWaves) void paged_extend_kernel(
 // unit of the workgroup slot piece_slots[j] (z << 8 | x) names (each written by this launch, possibly
 // empty: max -inf, sum 0); one piece was stored by the main kernel.  All of a chunk's partials are
 // requested before the first use.
+// `uncovered`: the plan's pieces do not reach the context's end (a plan built from other lengths);
+// the rows are then written as NaN.  A piece entry outside the launch (-1, or a slot past the batch or
+// the split count) is read from the sequence's own first slot with weight 0 and also makes the rows NaN.
 __device__ __forceinline__ void merge_planned(const float* __restrict__ part_o, const float* __restrict__ part_ml,
-                                              int pieces, const int32_t* __restrict__ piece_slots, int b, int KV,
-                                              int kvh, int splits, int rr, int d0, uint32_t* dst) {
+                                              int pieces, const int32_t* __restrict__ piece_slots, int b,
+                                              int batch, int KV, int kvh, int splits, bool uncovered, int rr,
+                                              int d0, uint32_t* dst) {
   constexpr int kChunk = 8;
   if (pieces <= 1) return;
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  bool bad = uncovered;
   for (int c0 = 0; c0 < pieces; c0 += kChunk) {
     f32x2 ml[kChunk];
     f32x4 v[kChunk];
     int64_t unit[kChunk];
+    bool ok[kChunk];
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {  // past the last piece: the last, weight 0 below
       const int jj = min(c0 + j, pieces - 1);
       // The first `splits` pieces sit in the sequence's own slots; later ones in the slots that took them.
-      const int e = jj < splits ? (b << 8) | jj : piece_slots[jj];
+      int e = jj < splits ? (b << 8) | jj : piece_slots[jj];
+      ok[j] = e >= 0 && (e >> 8) < batch && (e & 255) < splits;
+      if (!ok[j]) e = b << 8;
       unit[j] = ((int64_t)(e >> 8) * KV + kvh) * splits + (e & 255);
     }
 #pragma unroll
@@ -598,7 +612,8 @@ __device__ __forceinline__ void merge_planned(const float* __restrict__ part_o, 
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
-      const float mj = c0 + j < pieces ? ml[j][0] : -INFINITY;
+      bad |= c0 + j < pieces && !ok[j];
+      const float mj = c0 + j < pieces && ok[j] ? ml[j][0] : -INFINITY;
       const float mn = fmaxf(m, mj);
       const float mu = (mn == -INFINITY) ? 0.f : mn;
       const float a = exp2f(m - mu), w = exp2f(mj - mu);
@@ -607,7 +622,7 @@ __device__ __forceinline__ void merge_planned(const float* __restrict__ part_o, 
       m = mn;
     }
   }
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const float inv = bad ? __builtin_nanf("") : l > 0.f ? 1.0f / l : 0.f;
   dst[0] = pack_bf(acc[0] * inv, acc[1] * inv);
   dst[1] = pack_bf(acc[2] * inv, acc[3] * inv);
 }
@@ -640,10 +655,13 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
   const int per_row = (kD / 4) >> shift;
   const int rr = threadIdx.x / per_row;
   const int d0 = (int)blockIdx.z * (kD >> shift) + (threadIdx.x & (per_row - 1)) * 4;
-  if constexpr (kPlanned) {
+  // A plan written for another launch (header: batch, splits) is ignored, as the main kernel ignores it.
+  if (kPlanned && plan[0] == (int)gridDim.y && plan[1] == splits) {
     const int pieces = min(max(plan[kPlanHead + b], 1), 2 * splits);
+    const int L = min(seq_lens[b], max_seq_len);
+    const int span = min(((L + pieces - 1) / pieces + 31) / 32 * 32, ((max_seq_len + splits - 1) / splits + 31) / 32 * 32);
     merge_planned(part_o, part_ml, pieces, plan + kPlanHead + (int)gridDim.y * (1 + splits) + b * 2 * splits, b,
-                  KV, kvh, splits, rr, d0,
+                  (int)gridDim.y, KV, kvh, splits, (int64_t)pieces * span < L, rr, d0,
                   out_vec(out, (int64_t)b * S + rr / G, (kvh * G + rr % G) * kD + d0, H * kD, out_packed));
     return;
   }
@@ -699,9 +717,10 @@ __global__ __launch_bounds__(kPartRows * kD / 4) void paged_extend_merge_kernel(
 // for which the pieces fit the slots (each context at least one piece, at most 2 * splits).
 // Slot (sequence z, x) takes piece x of context z while z has that many; the slots a short
 // context leaves spare take, in order, the pieces past `splits` of the long ones; any left over
-// stay idle.  Layout: [1, splits, pieces of each sequence (B), slot entries (B * splits): sequence << 8 |
+// stay idle.  Layout: [batch, splits, pieces of each sequence (B), slot entries (B * splits): sequence << 8 |
 // piece, or -1 for idle; then per sequence 2 * splits piece entries: the slot z << 8 | x that takes the
-// piece (-1 past the sequence's pieces)].  A workgroup writes its partial at its own slot's unit, so
+// piece (-1 past the sequence's pieces)], where the header [batch, splits] names the launch the plan is
+// for (the attention kernels ignore a plan whose header differs).  A workgroup writes its partial at its own slot's unit, so
 // the workspace is that of an even launch.
 constexpr int kPlanMaxBatch = 256;
 constexpr int kPlanThreads = 256;
@@ -745,7 +764,7 @@ __global__ __launch_bounds__(kPlanThreads) void paged_extend_plan_kernel(const i
     }
     s_spare[batch] = sp;
     s_over[batch] = ov;
-    plan[0] = 1;
+    plan[0] = batch;
     plan[1] = splits;
   }
   __syncthreads();

@@ -153,8 +153,8 @@ class _BucketedStep:
 
 def _decode_forward(language: LanguageModel, cache: KVCache, buffers: StepBuffers, logits: torch.Tensor,
                     st: _BucketedStep, bucket: int) -> tuple[torch.Tensor, torch.Tensor]:
-    batch = DecodeBatch(st.ids[:bucket], st.positions[:bucket], st.slots[:bucket], st.seq_lens[:bucket],
-                        st.table[:bucket])
+    batch = DecodeBatch(None, st.positions[:bucket], st.slots[:bucket], st.seq_lens[:bucket], st.table[:bucket],
+                        ids=st.ids[:bucket])
     hidden = language.decode(batch, cache, buffers)
     tokens, out = lm_head.lm_head_argmax(hidden, language.weights.lm_head, predicted=buffers.predicted[:bucket],
                                          logits=logits[:bucket], return_logits=True,
@@ -165,8 +165,8 @@ def _decode_forward(language: LanguageModel, cache: KVCache, buffers: StepBuffer
 def _extend_forward(language: LanguageModel, cache: KVCache, buffers: StepBuffers, st: _BucketedStep,
                     bucket: int) -> torch.Tensor:
     s = st.s
-    batch = ExtendBatch(st.ids[: bucket * s], st.positions[: bucket * s], st.slots[: bucket * s],
-                        st.seq_lens[:bucket], st.table[:bucket], s)
+    batch = ExtendBatch(None, st.positions[: bucket * s], st.slots[: bucket * s], st.seq_lens[:bucket],
+                        st.table[:bucket], s, ids=st.ids[: bucket * s])
     hidden = language.extend(batch, cache, buffers)
     return language.greedy(hidden, buffers).view(bucket, s)
 
@@ -336,8 +336,8 @@ class VerifyLoop:
             self.tokens_per_seq, max_n=self.max_n, max_tokens=self.max_tokens, max_positions=self.max_positions,
             out=self.inputs,
         )
-        batch = ExtendBatch(inp.ids, inp.positions, inp.slots, inp.attn_seq_lens, self.block_table,
-                            self.tokens_per_seq)
+        batch = ExtendBatch(None, inp.positions, inp.slots, inp.attn_seq_lens, self.block_table,
+                            self.tokens_per_seq, ids=inp.ids)
         hidden = self.language.extend(batch, self.cache, self.buffers)
         state = dict(seq_len=self.seq_len, history=self.history, history_len=self.history_len, eos_id=self.eos_id,
                      max_tokens=self.max_tokens, finished=self.finished, out=self.accepted)

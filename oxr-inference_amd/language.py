@@ -193,36 +193,56 @@ def random_weights(config: LanguageConfig, max_positions: int, *, seed: int = 0,
                            mat(c.vocab_size, c.hidden_size), cos.to(device), sin.to(device))
 
 
+def _check_batch_inputs(embeds: torch.Tensor | None, ids: torch.Tensor | None, what: str) -> None:
+    """Exactly one of ``embeds`` (bf16 rows, the reference's field) and ``ids`` (int64 token ids)."""
+    if (embeds is None) == (ids is None):
+        raise ValueError(f"{what}: give either embeds (bf16 [T, hidden]) or ids= (int64 [T]), not both or neither")
+    if ids is not None and ids.dtype != torch.int64:
+        raise TypeError(f"{what}: ids must be int64 token ids, got {ids.dtype}")
+    if embeds is not None and embeds.dtype != torch.bfloat16:
+        hint = " (token ids go in ids=)" if not embeds.is_floating_point() else ""
+        raise TypeError(f"{what}: embeds must be bf16 [T, hidden], got {embeds.dtype}{hint}")
+
+
 @dataclass
 class ExtendBatch:
     """One verify step: every sequence brings the same number S of new tokens (language.py:122-136).
 
-    The reference passes ``embeds``; this build takes the token ``ids`` and fuses the embedding
-    gather into the first norm (``embeds`` may be given instead)."""
+    The fields keep the reference's order, so the reference's callers build it unchanged:
+    ``ExtendBatch(embed_tokens(ids), positions, slots, seq_lens, block_table, S)`` (engine.py:716-724,
+    decode_graph.py:163-166).  This build's own callers pass ``embeds=None`` and the token ids as
+    ``ids=``: the embedding gather then runs inside layer 0's input norm (one launch fewer)."""
 
-    ids: torch.Tensor | None  # int64 [B * S]
+    embeds: torch.Tensor | None  # bf16 [B * S, hidden]
     positions: torch.Tensor   # int64 [B * S]
     slots: torch.Tensor       # int64 [B * S]
     seq_lens: torch.Tensor    # int32 [B], including the S new tokens
     block_table: torch.Tensor  # int32 [B, max_blocks]
     tokens_per_seq: int
-    embeds: torch.Tensor | None = None  # bf16 [B * S, hidden]
+    ids: torch.Tensor | None = None  # int64 [B * S], in place of embeds
+
+    def __post_init__(self) -> None:
+        _check_batch_inputs(self.embeds, self.ids, "ExtendBatch")
 
 
 @dataclass
 class DecodeBatch:
-    """One decode step: one new token per sequence (language.py:54-66).  As with
-    :class:`ExtendBatch`, token ``ids`` replace the reference's ``embeds`` (which may still be given)."""
+    """One decode step: one new token per sequence (language.py:54-66), fields in the reference's order
+    (``DecodeBatch(embed_tokens(ids), positions, slots, seq_lens, block_table)``, engine.py:594-600);
+    as with :class:`ExtendBatch`, ``ids=`` may replace ``embeds``."""
 
-    ids: torch.Tensor | None  # int64 [B]
+    embeds: torch.Tensor | None  # bf16 [B, hidden]
     positions: torch.Tensor   # int64 [B]
     slots: torch.Tensor       # int64 [B]
     seq_lens: torch.Tensor    # int32 [B], including the new token
     block_table: torch.Tensor  # int32 [B, max_blocks]
-    embeds: torch.Tensor | None = None  # bf16 [B, hidden]
+    ids: torch.Tensor | None = None  # int64 [B], in place of embeds
+
+    def __post_init__(self) -> None:
+        _check_batch_inputs(self.embeds, self.ids, "DecodeBatch")
 
     def as_extend(self) -> ExtendBatch:
-        return ExtendBatch(self.ids, self.positions, self.slots, self.seq_lens, self.block_table, 1, self.embeds)
+        return ExtendBatch(self.embeds, self.positions, self.slots, self.seq_lens, self.block_table, 1, ids=self.ids)
 
 
 @dataclass
@@ -311,6 +331,21 @@ class LanguageModel:
         ``paged_decode``."""
         return self.extend(batch.as_extend(), cache, buffers)
 
+    def embed_tokens(self, ids: torch.Tensor) -> torch.Tensor:
+        """The reference's ``embed_tokens`` module (an ``nn.Embedding``, language.py:155) as its eager
+        decode and verify paths call it (engine.py:595, 717): bf16 ``[*ids.shape, hidden]``, the
+        embedding table's rows of integer ``ids``.  Ids outside ``[0, vocab)`` are clamped (the
+        reference's callers clamp negative ids themselves, model.py:32)."""
+        if ids.dtype not in (torch.int64, torch.int32):
+            raise TypeError(f"embed_tokens: ids must be int64 or int32, got {ids.dtype}")
+        _lib.require_gpu(ids, name="embed_tokens")
+        c, table = self.config, self.weights.embed
+        flat = ids.reshape(-1).to(torch.int64).contiguous()
+        out = torch.empty(flat.numel(), c.hidden_size, dtype=torch.bfloat16, device=ids.device)
+        _lib.call("oxr_embed_gather", flat.data_ptr(), flat.numel(), table.data_ptr(), c.vocab_size, c.hidden_size,
+                  out.data_ptr(), c.hidden_size, _lib.stream(ids.device))
+        return out.view(*ids.shape, c.hidden_size)
+
     def _buffers(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers | None) -> StepBuffers:
         _lib.require_gpu(batch.positions, batch.slots, batch.seq_lens, batch.block_table, name="extend")
         b, s = batch.block_table.shape[0], batch.tokens_per_seq
@@ -321,7 +356,8 @@ class LanguageModel:
         return buffers
 
     def embed(self, batch: ExtendBatch, buffers: StepBuffers) -> None:
-        """residual = embed_tokens(ids) (decode_graph.py:164); h = layer 0's input norm of it."""
+        """residual = embed_tokens(ids) (decode_graph.py:164), or the caller's ``embeds``; h = layer 0's
+        input norm of it."""
         buffers.pending_splits = 0
         c, w = self.config, self.weights
         t = batch.block_table.shape[0] * batch.tokens_per_seq
@@ -332,6 +368,8 @@ class LanguageModel:
                       w.layers[0].input_norm.data_ptr(), float(c.rms_norm_eps), res.data_ptr(),
                       buffers.h_packed.data.data_ptr(), 1, stream)
         else:
+            _lib.require(tuple(batch.embeds.shape) == (t, c.hidden_size),
+                         f"extend: embeds has shape {tuple(batch.embeds.shape)}, expected {(t, c.hidden_size)}")
             res.copy_(batch.embeds)
             self._norm(res, w.layers[0].input_norm, buffers.h_packed.view_rows(t), stream)
 

@@ -252,7 +252,17 @@ class NgramProposer:
         self._mirrored = n
 
     def extend(self, tokens: Sequence[int], old_length: int) -> None:
-        """``tokens`` from ``old_length`` on are new; index them (speculative.py:28-31)."""
+        """``tokens`` from ``old_length`` on are new; index them (speculative.py:28-31).
+
+        The reference adds positions ``[max(old_length, 1), len(tokens))`` to its dict.  The device
+        index is a prefix of the history (every position below ``index_len``), which is the same
+        set whenever ``old_length`` does not skip past what is already indexed: then the union is
+        ``[1, len(tokens))`` and each n-gram's latest position is its maximum, as in the dict.  An
+        ``old_length`` beyond the indexed length would leave a gap the prefix cannot express, so it
+        raises ``ValueError`` (the engine always passes the previous length, engine.py:677-681)."""
+        if old_length > self._indexed:
+            raise ValueError(f"extend: old_length {old_length} would leave positions [{self._indexed}, {old_length}) "
+                             "unindexed; the device index covers a prefix of the history")
         self._indexed = max(self._indexed, len(tokens))
         self._sync(tokens)
 

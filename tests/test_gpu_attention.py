@@ -26,6 +26,31 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+def _inputs(seq_lens, S, H, KV, block_size, num_blocks, seed, table_width=None):
+    """q, caches, lengths and table on the GPU, and each sequence's visible K/V rows (bits) for the oracle."""
+    rng = np.random.default_rng(seed)
+    B = len(seq_lens)
+    seq_lens = np.asarray(seq_lens, dtype=np.int32)
+    need = (seq_lens + block_size - 1) // block_size
+    width = table_width or int(need.max())
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    table = np.full((B, width), -7, dtype=np.int32)
+    off = 0
+    for b in range(B):
+        table[b, : need[b]] = perm[off : off + need[b]]
+        off += need[b]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    vc = torch.randn(num_blocks, block_size, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn(B, S, H, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k_rows, v_rows = [], []
+    for b in range(B):
+        blocks = torch.from_numpy(table[b, : need[b]].astype(np.int64)).cuda()
+        k_rows.append(_bits(kc[blocks].flatten(0, 1)[: seq_lens[b]]))
+        v_rows.append(_bits(vc[blocks].flatten(0, 1)[: seq_lens[b]]))
+    return q, kc, vc, torch.from_numpy(seq_lens).cuda(), torch.from_numpy(table).cuda(), k_rows, v_rows
+
+
 def _run(seq_lens, S, H, KV, block_size, num_blocks, seed, table_width=None, max_seq_len=None, planned=False):
     rng = np.random.default_rng(seed)
     B = len(seq_lens)
@@ -116,7 +141,7 @@ def test_plan_covers_every_piece_once(seq_lens, S, H, KV) -> None:
     assert plan is not None
     p = plan.cpu().numpy()
     splits = int(p[1])
-    assert p[0] == 1 and splits > 1 and p.size == 2 + B + 3 * B * splits
+    assert p[0] == B and splits > 1 and p.size == 2 + B + 3 * B * splits
     pieces = p[2 : 2 + B]
     slots = p[2 + B : 2 + B + B * splits].reshape(B, splits)
     piece_slots = p[2 + B + B * splits :].reshape(B, 2 * splits)
@@ -201,3 +226,50 @@ def test_query_row_tiles(S, H, KV) -> None:
     and 7 rows take the split merge in two dim slices (8 and more rows: four; fewer than 4: one)."""
     announce("attention row tiles", S, H, KV)
     _run([S, S + 1, 700, 3000], S, H, KV, 16, 1024, seed=39 + S + H)
+
+
+def test_plan_for_another_launch_is_ignored() -> None:
+    """A plan whose header names another split count (written for a longer max_seq_len) or another
+    batch (same split count) is ignored: the launch runs on even pieces, bit-identical to the launch
+    without a plan, and reads nothing outside its arrays."""
+    # max_seq_len 1024 gives 4 splits (at least 256 keys each); a plan for 4096 has the batch's 8.
+    lens = [5, 33, 1000, 700, 1024, 200, 64, 512]
+    q, kc, vc, lens_t, table, _, _ = _inputs(lens, 4, 16, 8, 16, 4096, seed=41)
+    announce("attention plan of another launch")
+    even = attention.paged_extend(q, kc, vc, lens_t, table, max_seq_len=1024)
+    other_splits = attention.build_plan(lens_t, 4, 16, 8, 4096)
+    own = attention.build_plan(lens_t, 4, 16, 8, 1024)
+    torch.cuda.synchronize()
+    assert int(other_splits[1]) != int(own[1])
+    got = attention.paged_extend(q, kc, vc, lens_t, table, max_seq_len=1024, plan=other_splits)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(got), _bits(even))
+    # max_seq_len 512 caps both batches at 2 splits; the plan was written for 16 sequences.
+    short = [min(n, 512) for n in lens]
+    q, kc, vc, lens_t, table, _, _ = _inputs(short, 4, 16, 8, 16, 4096, seed=42)
+    even = attention.paged_extend(q, kc, vc, lens_t, table, max_seq_len=512)
+    other_batch = attention.build_plan(torch.cat([lens_t, lens_t.flip(0)]), 4, 16, 8, 512)
+    mine = attention.build_plan(lens_t, 4, 16, 8, 512)
+    torch.cuda.synchronize()
+    assert int(other_batch[0]) == 16 and int(other_batch[1]) == int(mine[1])
+    got = attention.paged_extend(q, kc, vc, lens_t, table, max_seq_len=512, plan=other_batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(got), _bits(even))
+
+
+def test_plan_from_shorter_lengths_gives_nan_rows() -> None:
+    """A plan written from shorter contexts than the launch's (same batch and split count): the
+    sequence whose planned pieces cannot reach its last key gets NaN rows instead of silently
+    dropped keys; sequences the plan still covers match the oracle."""
+    built_for = [20] * 8  # one piece each: the 4000-key context cannot fit one even piece
+    lens = [100] * 7 + [4000]
+    q, kc, vc, lens_t, table, k_rows, v_rows = _inputs(lens, 4, 16, 8, 16, 4096, seed=43, table_width=256)
+    announce("attention stale plan")
+    plan = attention.build_plan(torch.tensor(built_for, dtype=torch.int32, device="cuda"), 4, 16, 8, 4096)
+    out = attention.paged_extend(q, kc, vc, lens_t, table, max_seq_len=4096, plan=plan)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isnan(got[7]).all()
+    exact, _ = oracle_attention.paged_extend(_bits(q[:7]), k_rows[:7], v_rows[:7], 128 ** -0.5)
+    err = np.abs(got[:7] - exact)
+    assert (err <= ATOL + RTOL * np.abs(exact)).all(), err.max()

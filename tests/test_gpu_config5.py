@@ -99,8 +99,8 @@ def test_teacher_forced_layer(model, layer) -> None:
     t = B * S
     x = (torch.randn(t, CONFIG.hidden_size, generator=torch.Generator().manual_seed(layer)) * 0.5).to(torch.bfloat16)
     d = lambda a, dt: torch.from_numpy(np.asarray(a)).to(dt).cuda()
-    eb = language.ExtendBatch(d(np.arange(t), torch.int64), d(pb.positions, torch.int64), d(pb.slots, torch.int64),
-                              d(pb.seq_lens, torch.int32), d(pb.block_table, torch.int32), S)
+    eb = language.ExtendBatch(None, d(pb.positions, torch.int64), d(pb.slots, torch.int64),
+                              d(pb.seq_lens, torch.int32), d(pb.block_table, torch.int32), S, ids=d(np.arange(t), torch.int64))
     # The oracle gets only the pages the batch uses, renumbered.
     used = np.unique(pb.block_table)
     remap = np.zeros(pool, dtype=np.int64)
@@ -143,6 +143,24 @@ def _margins(logits: torch.Tensor) -> np.ndarray:
     values = logits.float().numpy()
     part = np.partition(values, -2, axis=-1)
     return part[:, -1] - part[:, -2]
+
+
+# Per sequence and per row, the GPU's logit error against unrounded arithmetic relative to the
+# oracle's for the same sequence / row.  The global ratio above averages over every row; these
+# catch an error confined to one sequence (a lost context piece gives O(0.1-1) logit errors, ten
+# or more times the oracle's 0.04) or to one row.  A row's error is a sum of many independent
+# roundings, so its ratio scatters more than the sequence's.
+SEQ_ERROR_RATIO = 1.6
+ROW_ERROR_RATIO = 2.5
+
+
+def _local_errors(err_gpu: torch.Tensor, err_ref: torch.Tensor, rows_per_seq: int) -> tuple[float, float]:
+    """Worst per-sequence and per-row ratios of the GPU's RMS logit error to the oracle's."""
+    row_g = err_gpu.pow(2).mean(-1).sqrt()
+    row_r = err_ref.pow(2).mean(-1).sqrt()
+    seq_g = err_gpu.view(-1, rows_per_seq * err_gpu.shape[-1]).pow(2).mean(-1).sqrt()
+    seq_r = err_ref.view(-1, rows_per_seq * err_ref.shape[-1]).pow(2).mean(-1).sqrt()
+    return (seq_g / seq_r).max().item(), (row_g / row_r).max().item()
 
 
 def _loop_case(m, B: int, ctx: tuple[int, int], seed: int, steps: int):
@@ -224,7 +242,10 @@ def test_verify_loop_full_size(model, B, ctx) -> None:
         print(f"B={B} ctx={ctx} step {step}: logit RMS error vs unrounded: gpu {rms(err_gpu):.4f}, oracle "
               f"{rms(err_ref):.4f}; gpu-oracle max {(got_logits.float() - want.logits.float()).abs().max().item():.3f}; "
               f"clear rows {clear.mean():.2f}; ids differ at {differ.tolist()} (margins {margin[differ].round(3).tolist()})")
+        seq_ratio, row_ratio = _local_errors(err_gpu, err_ref, S)
+        print(f"  worst per-sequence error ratio {seq_ratio:.3f}, per-row {row_ratio:.3f}")
         assert rms(err_gpu) <= ERROR_RATIO * rms(err_ref)
+        assert seq_ratio <= SEQ_ERROR_RATIO and row_ratio <= ROW_ERROR_RATIO
         assert np.array_equal(got_pred[clear], want_pred[clear])
 
         taken, new_lens = oracle_decoder.accept_step(want.drafts, got_pred.reshape(B, S), lens)
@@ -238,3 +259,59 @@ def test_verify_loop_full_size(model, B, ctx) -> None:
         lens = new_lens
     del loop, cache
     torch.cuda.empty_cache()
+
+
+def test_decode_graphs_full_size(model) -> None:
+    """``DecodeGraphs`` (decode_graph.py:33-119) at the benchmark's shape: the 28-layer model, 8
+    sequences with one new token each after 4096 context keys, pages from a permuted pool.  Logits
+    and greedy ids against ``oracle.decoder.extend`` with one token per sequence, under the verify
+    loop's criterion: RMS logit error against unrounded arithmetic at most ERROR_RATIO x the
+    oracle's (and per sequence / per row as above); ids equal wherever the oracle's top-2 margin
+    exceeds MARGIN_FACTOR x its RMS error; and the graph's ids are exactly the argmax of its logits."""
+    m, cpu_w = model
+    B, ctx = 8, 4096
+    rng = np.random.default_rng(777)
+    width = -(-(ctx + 1) // BS) + 1
+    num_blocks = B * width + 16
+    cache = kv_cache.KVCache(CONFIG.num_layers, CONFIG.num_kv_heads, CONFIG.head_dim, num_blocks, block_size=BS)
+    g = torch.Generator(device="cuda").manual_seed(777)
+    for layer in range(CONFIG.num_layers):
+        cache.k[layer].normal_(generator=g)
+        cache.v[layer].normal_(generator=g)
+    announce("config 5 decode graphs", B, ctx)
+    graphs = decode_graph.DecodeGraphs(m, cache, max_batch=B, max_positions=width * BS)
+    pages = [p for p in rng.permutation(num_blocks).tolist() if p != graphs.scratch_block]
+    tables = [pages[width * b : width * (b + 1)] for b in range(B)]
+    ids = rng.integers(0, CONFIG.vocab_size, size=B).tolist()
+    positions = [ctx] * B
+    slots = [tables[b][ctx // BS] * BS + ctx % BS for b in range(B)]
+    seq_lens = [ctx + 1] * B
+    cpu_k, cpu_v = cache.k.cpu(), cache.v.cpu()
+    logits, tokens = graphs.run(ids, positions, slots, seq_lens, tables)
+    got_logits, got_ids = logits.cpu(), tokens.cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.array_equal(got_ids, got_logits.float().argmax(-1).numpy())
+    table = torch.tensor(tables, dtype=torch.int32)
+    announce("config 5 decode graphs: oracle")
+    want_hidden = oracle_decoder.extend(CONFIG, cpu_w, torch.tensor(ids), torch.tensor(positions), torch.tensor(slots),
+                                        torch.tensor(seq_lens, dtype=torch.int32), table, 1, cpu_k.clone(),
+                                        cpu_v.clone())
+    want_logits = oracle_decoder.logits(cpu_w, want_hidden)
+    _, exact = unrounded.extend(CONFIG, cpu_w, ids, positions, seq_lens, table.numpy(), 1, cpu_k, cpu_v, BS,
+                                dtype=torch.float32, with_logits=True)
+    rms = lambda e: e.pow(2).mean().sqrt().item()
+    err_gpu = got_logits.float() - exact
+    err_ref = want_logits.float() - exact
+    margin = _margins(want_logits)
+    want_ids = want_logits.float().argmax(-1).numpy()
+    clear = margin > MARGIN_FACTOR * rms(err_ref)
+    seq_ratio, row_ratio = _local_errors(err_gpu, err_ref, 1)
+    print(f"decode B={B} ctx={ctx}: logit RMS error vs unrounded: gpu {rms(err_gpu):.4f}, oracle {rms(err_ref):.4f}; "
+          f"worst row ratio {row_ratio:.3f}; clear rows {clear.mean():.2f}; ids differ at "
+          f"{np.flatnonzero(got_ids != want_ids).tolist()}")
+    assert rms(err_gpu) <= ERROR_RATIO * rms(err_ref)
+    assert row_ratio <= ROW_ERROR_RATIO
+    assert np.array_equal(got_ids[clear], want_ids[clear])
+    del graphs, cache
+    torch.cuda.empty_cache()
+

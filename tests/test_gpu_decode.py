@@ -88,13 +88,14 @@ def test_decode_after_prefill_equals_full_sequence() -> None:
     slot = lambda b, p: int(table[b, p // bs]) * bs + p % bs
     announce("prefill then decode")
     for b, n in enumerate(lens):  # prefill sequence b alone: an extend of n tokens at positions 0..n-1
-        eb = language.ExtendBatch(d(toks[b][:n], torch.int64), d(np.arange(n), torch.int64),
+        eb = language.ExtendBatch(None, d(np.arange(n), torch.int64),
                                   d([slot(b, p) for p in range(n)], torch.int64), d([n], torch.int32),
-                                  d(table[b : b + 1], torch.int32), n)
+                                  d(table[b : b + 1], torch.int32), n, ids=d(toks[b][:n], torch.int64))
         model.extend(eb, cache)
-    db = language.DecodeBatch(d([t[-1] for t in toks], torch.int64), d(lens, torch.int64),
+    db = language.DecodeBatch(None, d(lens, torch.int64),
                               d([slot(b, n) for b, n in enumerate(lens)], torch.int64),
-                              d([n + 1 for n in lens], torch.int32), d(table, torch.int32))
+                              d([n + 1 for n in lens], torch.int32), d(table, torch.int32),
+                              ids=d([t[-1] for t in toks], torch.int64))
     hidden = model.decode(db, cache)
     torch.cuda.synchronize()
     for b, n in enumerate(lens):
@@ -156,8 +157,8 @@ def test_decode_graphs_match_eager_and_keep_padding_on_scratch(max_batch, n, buc
     table_t = torch.full((n, width), graphs.scratch_block, dtype=torch.int32, device="cuda")
     for b in range(n):
         table_t[b, : len(tables[b])] = torch.tensor(tables[b], dtype=torch.int32)
-    hidden = model.decode(language.DecodeBatch(d(ids, torch.int64), d(positions, torch.int64), d(slots, torch.int64),
-                                               d(seq_lens, torch.int32), table_t), cache)
+    hidden = model.decode(language.DecodeBatch(None, d(positions, torch.int64), d(slots, torch.int64),
+                                               d(seq_lens, torch.int32), table_t, ids=d(ids, torch.int64)), cache)
     want_tokens, want_logits = lm_head.lm_head_argmax(hidden, model.weights.lm_head, return_logits=True)
     torch.cuda.synchronize()
     assert torch.equal(tokens, want_tokens)

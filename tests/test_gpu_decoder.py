@@ -87,8 +87,8 @@ def _small_case(seed):
     cache = _cache(SMALL, 256, bs, seed=seed + 1)
     ids = rng.integers(0, SMALL.vocab_size, size=B * S)
     d = lambda a, dt: torch.from_numpy(np.asarray(a)).to(dt).cuda()
-    eb = language.ExtendBatch(d(ids, torch.int64), d(batch.positions, torch.int64), d(batch.slots, torch.int64),
-                              d(batch.seq_lens, torch.int32), d(batch.block_table, torch.int32), S)
+    eb = language.ExtendBatch(None, d(batch.positions, torch.int64), d(batch.slots, torch.int64),
+                              d(batch.seq_lens, torch.int32), d(batch.block_table, torch.int32), S, ids=d(ids, torch.int64))
     cpu_args = (torch.from_numpy(ids), torch.from_numpy(batch.positions), torch.from_numpy(batch.slots),
                 torch.from_numpy(batch.seq_lens), torch.from_numpy(batch.block_table), S)
     return model, cpu_w, cache, eb, cpu_args, batch
@@ -148,6 +148,34 @@ def test_extend_end_to_end_small_model() -> None:
     _ids_agree(pred, oracle_decoder.logits(cpu_w, want), margin_floor=0.1)
 
 
+def test_reference_eager_verify_sequence() -> None:
+    """The reference's eager verify fallback in its own form (engine.py:716-726): the batch built
+    positionally as ``ExtendBatch(language.embed_tokens(ids), positions, slots, seq_lens, table,
+    width)``, then ``extend`` -> ``logits`` -> ``argmax(-1).view(B, width)``.  ``embed_tokens`` gives
+    the table's rows exactly; the hidden state is bit-identical to the ``ids=`` form (the gather
+    fused into the first norm); both are checked against the oracle as the end-to-end test does."""
+    model, cpu_w, cache, eb_ids, cpu_args, _ = _small_case(4)
+    cpu_k, cpu_v = cache.k.cpu(), cache.v.cpu()
+    ids_cpu, positions, slots, seq_lens, table, width = cpu_args
+    B = table.shape[0]
+    announce("reference eager verify sequence")
+    embeds = model.embed_tokens(ids_cpu.cuda())
+    torch.cuda.synchronize()
+    assert embeds.dtype == torch.bfloat16 and tuple(embeds.shape) == (B * width, SMALL.hidden_size)
+    assert torch.equal(embeds.cpu(), cpu_w.embed[ids_cpu])
+    batch = language.ExtendBatch(embeds, positions.cuda(), slots.cuda(), seq_lens.cuda(), table.cuda(), width)
+    hidden = model.extend(batch, cache)
+    tokens = model.logits(hidden).argmax(dim=-1).view(B, width)
+    hidden_ids = model.extend(eb_ids, cache)  # same K/V rewritten at the same slots
+    torch.cuda.synchronize()
+    assert torch.equal(hidden.cpu(), hidden_ids.cpu())
+    want = oracle_decoder.extend(SMALL, cpu_w, *cpu_args, cpu_k, cpu_v)
+    err = (hidden.float().cpu() - want.float()).abs()
+    rel = (err.pow(2).sum() / want.float().pow(2).sum()).sqrt().item()
+    assert rel < 2e-2, rel
+    _ids_agree(tokens.reshape(-1).cpu().numpy(), oracle_decoder.logits(cpu_w, want), margin_floor=0.1)
+
+
 def test_chunked_extends_equal_full_sequence() -> None:
     """tests/test_language_fused.py:250-278 of the reference, on the GPU path."""
     rng = np.random.default_rng(3)
@@ -162,9 +190,9 @@ def test_chunked_extends_equal_full_sequence() -> None:
         rows = np.repeat(np.arange(B), S)
         slots = table[rows, pos // bs] * bs + pos % bs
         eb = language.ExtendBatch(
-            torch.from_numpy(tokens[:, start : start + S].reshape(-1)).cuda(), torch.from_numpy(pos).cuda(),
+            None, torch.from_numpy(pos).cuda(),
             torch.from_numpy(slots.astype(np.int64)).cuda(), torch.full((B,), start + S, dtype=torch.int32).cuda(),
-            torch.from_numpy(table).cuda(), S,
+            torch.from_numpy(table).cuda(), S, ids=torch.from_numpy(tokens[:, start : start + S].reshape(-1)).cuda(),
         )
         hidden = model.extend(eb, cache)
     torch.cuda.synchronize()
@@ -289,8 +317,9 @@ def test_extend_graphs_list_interface_matches_eager() -> None:
     table = np.full((n, 6), scratch, dtype=np.int32)
     for b in range(n):
         table[b] = tables[b]
-    eb = language.ExtendBatch(torch.tensor(ids).cuda(), torch.tensor(positions).cuda(), torch.tensor(slots).cuda(),
-                              torch.tensor(seq_lens, dtype=torch.int32).cuda(), torch.from_numpy(table).cuda(), s)
+    eb = language.ExtendBatch(None, torch.tensor(positions).cuda(), torch.tensor(slots).cuda(),
+                              torch.tensor(seq_lens, dtype=torch.int32).cuda(), torch.from_numpy(table).cuda(), s,
+                              ids=torch.tensor(ids).cuda())
     eager = model.greedy(model.extend(eb, cache)).view(n, s)
     torch.cuda.synchronize()
     assert torch.equal(tokens, eager)
@@ -370,8 +399,9 @@ def test_extend_graphs_reference_defaults(n) -> None:
         table[b, : len(tables[b])] = tables[b]
     cache.k.copy_(before_k)
     cache.v.copy_(before_v)
-    eb = language.ExtendBatch(torch.tensor(ids).cuda(), torch.tensor(positions).cuda(), torch.tensor(slots).cuda(),
-                              torch.tensor(seq_lens, dtype=torch.int32).cuda(), torch.from_numpy(table).cuda(), s)
+    eb = language.ExtendBatch(None, torch.tensor(positions).cuda(), torch.tensor(slots).cuda(),
+                              torch.tensor(seq_lens, dtype=torch.int32).cuda(), torch.from_numpy(table).cuda(), s,
+                              ids=torch.tensor(ids).cuda())
     eager = model.greedy(model.extend(eb, cache)).view(n, s)
     torch.cuda.synchronize()
     assert torch.equal(tokens, eager)

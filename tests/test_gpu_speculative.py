@@ -13,7 +13,8 @@ import pytest
 import torch
 
 from conftest import announce, pkg
-from oracle import ngram
+from oracle import bf16, ngram
+from oracle import lm_head as oracle_lm_head
 
 pytestmark = pytest.mark.gpu
 spec = pkg("speculative")
@@ -48,6 +49,26 @@ def test_list_api_known_answers() -> None:
     assert spec.accept([7, 8], [7, 8, 5]) == [7, 8, 5]
     assert spec.accept([7, 8], [1, 8, 5]) == [1]
     assert spec.accept([], [4]) == [4]
+
+
+def test_extend_sequences_match_reference_dict() -> None:
+    """Random sequences of extend calls, as the engine makes them (old_length = the previous length)
+    and re-indexing from an earlier old_length: drafts identical to the reference's dict."""
+    rng = np.random.default_rng(6)
+    announce("extend sequences")
+    for _ in range(10):
+        tokens = rng.integers(0, 4, size=int(rng.integers(2, 60))).tolist()
+        n0 = int(rng.integers(0, len(tokens)))
+        mine, ref = spec.NgramProposer(tokens[:n0]), ngram.NgramIndex(tokens[:n0])
+        length = n0
+        while length < len(tokens):
+            new = min(len(tokens), length + int(rng.integers(1, 6)))
+            old = length if rng.random() < 0.7 else int(rng.integers(0, length + 1))
+            mine.extend(tokens[:new], old)
+            ref.extend(tokens[:new], old)
+            length = new
+            for k in (1, 3):
+                assert mine.propose(tokens[:length], k) == ref.propose(tokens[:length], k)
 
 
 def test_stale_index_matches_reference_dict() -> None:
@@ -344,3 +365,56 @@ def test_greedy_accept_matches_separate_launches(B: int, S: int, vocab: int) -> 
         assert (acc[:-1] < k).any()
     if B > 1:
         assert acc[-1] == 0 and res.num_committed[-1].item() == 0  # started finished
+
+
+def _u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_greedy_accept_config4_against_exact_product() -> None:
+    """Config 4 through the step's real tail (``greedy_accept_batch``: the wide LM head over 256 token
+    rows, its argmax finished inside the acceptance launch): 64 sequences x 4 positions, vocab
+    151,936, k = 3, each draft id planted as the reference argmax of its row with p = 0.5.  Greedy
+    ids equal the oracle's argmax of the exact product wherever its top-2 margin exceeds 2e-2; the
+    acceptance is bit-exact against ``oracle.ngram.accept`` on the kernel's ids, and against the
+    oracle's own ids on every sequence whose rows are all decided by a clear margin; KV lengths
+    advance by the committed count (engine.py:729-737)."""
+    B, S, vocab, k, atol = 64, 4, 151_936, 3, 2e-2
+    rng = np.random.default_rng(404)
+    gen = torch.Generator(device="cuda").manual_seed(404)
+    hidden = torch.randn(B * S, 2048, device="cuda", generator=gen).to(torch.bfloat16)
+    weight = (torch.randn(vocab, 2048, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    announce("greedy accept config4: exact product")
+    exact = oracle_lm_head.logits_exact(_u16(hidden), _u16(weight))
+    ref_ids = oracle_lm_head.argmax(bf16.from_f32(exact.astype(np.float32))).reshape(B, S)
+    sure = (oracle_lm_head.top2_margin(exact) > atol).reshape(B, S)
+    draft = ref_ids[:, :k].copy()
+    miss = rng.random((B, k)) >= 0.5
+    other = rng.integers(0, vocab - 1, size=(B, k))
+    draft[miss] = other[miss] + (other[miss] >= ref_ids[:, :k][miss])  # a random id other than the argmax
+    draft = draft.astype(np.int32)
+    dlen = np.full(B, k, dtype=np.int32)
+    seq0 = rng.integers(1000, 9000, size=B).astype(np.int32)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    seq_len = d(seq0)
+    packed = gemm.pack_weight(weight)
+    ws = torch.empty(lm_head.workspace_bytes(B * S, vocab), dtype=torch.uint8, device="cuda")
+    pred = torch.full((B, S), -7, dtype=torch.int64, device="cuda")
+    announce("greedy accept config4: launch")
+    res = spec.greedy_accept_batch(hidden, packed, d(draft), d(dlen), predicted=pred, workspace=ws, seq_len=seq_len)
+    torch.cuda.synchronize()
+    got = pred.cpu().numpy()
+    assert sure.mean() > 0.8
+    assert np.array_equal(got[sure], ref_ids[sure])
+    accepted = res.accepted.cpu().numpy()
+    committed = res.committed.cpu().numpy()
+    num = res.num_committed.cpu().numpy()
+    for b in range(B):
+        taken = ngram.accept(draft[b].tolist(), got[b].tolist())
+        assert accepted[b] == len(taken) - 1 and num[b] == len(taken), b
+        assert committed[b, : num[b]].tolist() == taken, b
+        if sure[b].all():
+            assert taken == ngram.accept(draft[b].tolist(), ref_ids[b].tolist()), b
+    assert np.array_equal(seq_len.cpu().numpy(), seq0 + num)
+    assert (accepted == k).any() and (accepted == 0).any() and ((accepted > 0) & (accepted < k)).any()
+
