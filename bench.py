@@ -15,6 +15,7 @@ restatement of the same step on this host's cores).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
     python bench.py --pmc-driver      # only attention launches + a calibration copy, for rocprofv3 --pmc
+    python bench.py --step-driver     # only verify-step replays + a calibration copy, for rocprofv3 --pmc
 """
 
 from __future__ import annotations
@@ -399,6 +400,44 @@ def pmc_driver(config, model, cache, loop) -> None:
     log("pmc driver done")
 
 
+def step_driver(config, model, cache, loop, replays: int = 12) -> None:
+    """The verify step's graph replayed ``replays`` times, then five device copies of COPY_BYTES: the
+    workload of the per-kernel counter runs of the step (rocprofv3 --pmc).  Prints each step kernel's
+    algorithmic bytes per launch (weights and activations read once, outputs written once) at this
+    shape."""
+    c, b, s = config, loop.batch, loop.tokens_per_seq
+    t, h = b * s, c.hidden_size
+    bf, f4 = 2, 4
+    o_splits = gemm.partial_splits(h, c.num_heads * c.head_dim)
+    d_splits = gemm.partial_splits(h, c.intermediate_size)
+    kv_row = 2 * c.num_kv_heads * c.head_dim * bf  # K and V of one token
+    ctx = (loop.seq_len + s).to(torch.int64)
+    algorithmic = {
+        "qkv": c.qkv_size * h * bf + t * h * bf + t * c.qkv_size * bf,
+        "o_proj": h * c.num_heads * c.head_dim * bf + t * c.num_heads * c.head_dim * bf + o_splits * t * h * f4,
+        "gate_up": 2 * c.intermediate_size * h * bf + t * h * bf + t * c.intermediate_size * bf,
+        "down": h * c.intermediate_size * bf + t * c.intermediate_size * bf + d_splits * t * h * f4,
+        "add_partials_rms_norm": d_splits * t * h * f4 + 3 * t * h * bf + h * bf,
+        "attention_main": int(ctx.sum().item()) * kv_row + t * c.qkv_size * bf + t * c.num_heads * c.head_dim * bf
+                          + t * kv_row,
+        "lm_head": c.vocab_size * h * bf + t * h * bf,
+    }
+    print(json.dumps({"algorithmic_bytes_per_launch": algorithmic, "tokens": t, "o_splits": o_splits,
+                      "down_splits": d_splits, "context": ctx.cpu().tolist(), "replays": replays,
+                      "copy_bytes": COPY_BYTES}), flush=True)
+    loop.capture()
+    for i in range(replays):
+        loop.replay()
+        torch.cuda.synchronize()
+        log(f"step replay {i + 1} of {replays}")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("step driver done")
+
+
 def _cpu_model_name() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -493,6 +532,8 @@ def main() -> int:
     p.add_argument("--cpu-warmup", type=int, default=3)
     p.add_argument("--prefill-driver", action="store_true", help="only the prefill attention measurement")
     p.add_argument("--configs-driver", action="store_true", help="only the per-kernel configurations 1-4")
+    p.add_argument("--step-driver", action="store_true",
+                   help="only verify-step graph replays + a calibration copy, for per-kernel rocprofv3 --pmc runs")
     args = p.parse_args()
     if args.ctx_min is not None and not 1 <= args.ctx_min <= args.ctx:
         p.error("--ctx-min must be in [1, --ctx]")
@@ -532,6 +573,9 @@ def main() -> int:
     loaded_context = loop.seq_len.clone()
     if args.pmc_driver:
         pmc_driver(config, model, cache, loop)
+        return 0
+    if args.step_driver:
+        step_driver(config, model, cache, loop)
         return 0
     log("capturing graph")
     loop.capture()
