@@ -40,6 +40,7 @@ kv_cache = importlib.import_module(f"{PKG}.kv_cache")
 decode_graph = importlib.import_module(f"{PKG}.decode_graph")
 attention = importlib.import_module(f"{PKG}.attention")
 gemm = importlib.import_module(f"{PKG}.gemm")
+mlp = importlib.import_module(f"{PKG}.mlp")
 kernels = importlib.import_module(f"{PKG}.kernels")
 lm_head = importlib.import_module(f"{PKG}.lm_head")
 speculative = importlib.import_module(f"{PKG}.speculative")
@@ -409,19 +410,26 @@ def step_driver(config, model, cache, loop, replays: int = 12) -> None:
     t, h = b * s, c.hidden_size
     bf, f4 = 2, 4
     o_splits = gemm.partial_splits(h, c.num_heads * c.head_dim)
-    d_splits = gemm.partial_splits(h, c.intermediate_size)
+    one_launch_mlp = model.mlp_gate_up is not None and t <= mlp.MAX_ROWS
+    d_splits = mlp.SPLITS_OUT if one_launch_mlp else gemm.partial_splits(h, c.intermediate_size)
     kv_row = 2 * c.num_kv_heads * c.head_dim * bf  # K and V of one token
     ctx = (loop.seq_len + s).to(torch.int64)
     algorithmic = {
         "qkv": c.qkv_size * h * bf + t * h * bf + t * c.qkv_size * bf,
         "o_proj": h * c.num_heads * c.head_dim * bf + t * c.num_heads * c.head_dim * bf + o_splits * t * h * f4,
-        "gate_up": 2 * c.intermediate_size * h * bf + t * h * bf + t * c.intermediate_size * bf,
-        "down": h * c.intermediate_size * bf + t * c.intermediate_size * bf + d_splits * t * h * f4,
         "add_partials_rms_norm": d_splits * t * h * f4 + 3 * t * h * bf + h * bf,
         "attention_main": int(ctx.sum().item()) * kv_row + t * c.qkv_size * bf + t * c.num_heads * c.head_dim * bf
                           + t * kv_row,
         "lm_head": c.vocab_size * h * bf + t * h * bf,
     }
+    if one_launch_mlp:
+        # Weights once, o_proj's partials and the residual in, the new residual and 8 partials out (h and
+        # act move between the CUs of an XCD through its L2).
+        algorithmic["mlp_block"] = (3 * c.intermediate_size * h * bf + o_splits * t * h * f4 + 2 * t * h * bf + h * bf
+                                    + d_splits * t * h * f4)
+    else:
+        algorithmic["gate_up"] = 2 * c.intermediate_size * h * bf + t * h * bf + t * c.intermediate_size * bf
+        algorithmic["down"] = h * c.intermediate_size * bf + t * c.intermediate_size * bf + d_splits * t * h * f4
     print(json.dumps({"algorithmic_bytes_per_launch": algorithmic, "tokens": t, "o_splits": o_splits,
                       "down_splits": d_splits, "context": ctx.cpu().tolist(), "replays": replays,
                       "copy_bytes": COPY_BYTES}), flush=True)

@@ -201,6 +201,41 @@ int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits, int64_t r
                               int32_t out_packed, oxr_stream_t stream);
 
 /*
+ * The same with the residual read from residual_in and the sum stored to residual (the two may be
+ * the same buffer): the norm after oxr_mlp_block, which leaves the new residual in a second buffer.
+ */
+int oxr_add_partials_rms_norm_from(const float* partials, int32_t k_splits, int64_t rows, int64_t hidden,
+                                   const oxr_bf16* residual_in, oxr_bf16* residual, const oxr_bf16* weight,
+                                   float eps, oxr_bf16* out, int32_t out_packed, oxr_stream_t stream);
+
+/*
+ * A decoder layer's MLP block in one launch (DecoderLayer._mlp, language.py:266-269, with
+ * _add_rms_norm 94-99 and _silu_mul 102-104), for 1..32 token rows of the config-5 decoder
+ * (hidden 2048, intermediate 6144) on an MI355X in its single-partition mode (256 CUs, 8 XCDs):
+ *   residual_out = bf16(bf16(sum_s o_partials[s]) + residual_in)      (o_splits = 4 or 8 slices)
+ *   h = rms_norm(residual_out) * post_norm, as oxr_add_partials_rms_norm (same bits)
+ *   act = bf16(bf16(silu(bf16(h gate^T))) * bf16(h up^T))
+ *   partials_out[x] = act[:, 768 x : 768 x + 768] @ down[:, 768 x : 768 x + 768]^T, x = 0..7 (fp32
+ *   [8, rows, 2048], summed in slice order by the next oxr_add_partials_rms_norm[_from]).
+ * gate_up_interleaved: the fused gate_up weight [2 * 6144, 2048] with its rows interleaved by 8
+ * (row 16 j + i is gate row 8 j + i for i < 8, up row 8 j + i - 8 otherwise), then packed
+ * (oxr_pack_weight_bf16); down: down_proj [2048, 6144] packed.  residual_out must not be
+ * residual_in (every XCD reads each input row while one writes the output row).
+ * workspace: oxr_mlp_block_workspace_bytes() bytes, 256-byte aligned, zero before the first call;
+ * each call leaves its control words zero again, so one workspace serves every later call on its
+ * stream (calls that overlap on one GPU race).  Word 512 (uint32) of the workspace is an error
+ * word the kernel ORs into when workgroup placement or a wait inside the launch fails (the
+ * launch then ends with undefined outputs); it stays set until the caller clears it.
+ * OXR_ERR_UNSUPPORTED for other shapes or devices (oxr_mlp_block_supported says which).
+ */
+size_t oxr_mlp_block_workspace_bytes(void);
+int oxr_mlp_block_supported(int64_t rows, int64_t hidden, int64_t intermediate, int32_t o_splits);
+int oxr_mlp_block(const float* o_partials, int32_t o_splits, const oxr_bf16* residual_in, int64_t rows,
+                  int64_t hidden, int64_t intermediate, const oxr_bf16* post_norm, float eps,
+                  const oxr_bf16* gate_up_interleaved, const oxr_bf16* down, oxr_bf16* residual_out,
+                  float* partials_out, void* workspace, size_t workspace_bytes, oxr_stream_t stream);
+
+/*
  * (3) Multi-query causal paged attention of the verify step.
  * Replaces attention.paged_extend (oxr_runtime/attention.py:96-109); math as
  * the reference test stub (tests/test_language_fused.py:19-28, 50-57):

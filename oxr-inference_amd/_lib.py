@@ -69,6 +69,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "oxr_embed_rms_norm": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _F32, _P, _P, _I32, _P]),
     "oxr_embed_gather": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "oxr_add_partials_rms_norm": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _F32, _P, _I32, _P]),
+    "oxr_add_partials_rms_norm_from": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _P, _F32, _P, _I32, _P]),
+    "oxr_mlp_block_workspace_bytes": (ctypes.c_size_t, []),
+    "oxr_mlp_block_supported": (ctypes.c_int, [_I64, _I64, _I64, _I32]),
+    "oxr_mlp_block": (ctypes.c_int, [_P, _I32, _P, _I64, _I64, _I64, _P, _F32, _P, _P, _P, _P, _P, _SZ, _P]),
     "oxr_gemm_bf16": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _I32, _P, _I64, _P]),
     "oxr_gemm_bf16_partial_splits": (ctypes.c_int32, [_I64, _I64]),
     "oxr_gemm_bf16_partial": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P]),

@@ -26,7 +26,8 @@ enum Source { kRows = 0, kEmbed = 1, kAddPartials = 2 };
 // weights are fetched at the same time.  MODE kRows: x is [rows, ldx].
 // kEmbed: row = table[ids[row]], also stored as the residual.  kAddPartials:
 // row = bf16(bf16(sum of the k-split fp32 partials of the GEMM that produced
-// it) + residual), stored back as the residual (the add of _add_rms_norm,
+// it) + residual), stored as the residual (read from x when given, else from
+// `residual` itself; the add of _add_rms_norm,
 // language.py:94-99, with the GEMM's bf16 output rounding first, as the
 // reference's nn.Linear does).
 template <int MODE, int SPLITS>
@@ -46,7 +47,7 @@ __global__ __launch_bounds__(kMaxThreads) void rms_norm_kernel(const bf16_t* __r
     id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // stay inside the table
     src = x + id * ldx;
   } else if constexpr (MODE == kAddPartials) {
-    src = residual + (int64_t)row * ldo;
+    src = (x ? x : residual) + (int64_t)row * ldo;  // x: the residual to read, when not `residual` itself
   } else {
     src = x + (int64_t)row * ldx;
   }
@@ -169,6 +170,19 @@ extern "C" int oxr_add_partials_rms_norm(const float* partials, int32_t k_splits
   OXR_RETURN_IF(!partials || !residual || !weight || !out, OXR_ERR_INVALID_ARG);
   return launch<kAddPartials>(nullptr, hidden, nullptr, 0, partials, k_splits, (int)rows, (int)hidden, weight, eps,
                               residual, out, hidden, out_packed ? 1 : 0, (hipStream_t)stream);
+}
+
+extern "C" int oxr_add_partials_rms_norm_from(const float* partials, int32_t k_splits, int64_t rows, int64_t hidden,
+                                              const oxr_bf16* residual_in, oxr_bf16* residual, const oxr_bf16* weight,
+                                              float eps, oxr_bf16* out, int32_t out_packed, oxr_stream_t stream) {
+  using namespace oxr;
+  int st = check(rows, hidden, hidden, hidden);
+  if (st) return st;
+  OXR_RETURN_IF(k_splits < 1, OXR_ERR_INVALID_ARG);
+  if (rows == 0) return OXR_OK;
+  OXR_RETURN_IF(!partials || !residual_in || !residual || !weight || !out, OXR_ERR_INVALID_ARG);
+  return launch<kAddPartials>(residual_in, hidden, nullptr, 0, partials, k_splits, (int)rows, (int)hidden, weight,
+                              eps, residual, out, hidden, out_packed ? 1 : 0, (hipStream_t)stream);
 }
 
 extern "C" int oxr_embed_gather(const int64_t* ids, int64_t rows, const oxr_bf16* table, int64_t vocab, int64_t hidden,

@@ -196,14 +196,22 @@ def linear_partial(x: Rows, w: Weight, partials: torch.Tensor) -> int:
 
 
 def add_partials_rms_norm(partials: torch.Tensor, splits: int, residual: torch.Tensor, weight: torch.Tensor,
-                          eps: float, out: Rows) -> Rows:
+                          eps: float, out: Rows, *, residual_in: torch.Tensor | None = None) -> Rows:
     """``residual = bf16(bf16(sum of partials) + residual)``; ``out = rms_norm(residual) * weight``
     (``_add_rms_norm``, language.py:94-99, taking a ``linear_partial`` result).  ``out`` may be a
-    :class:`PackedMatrix` (the next GEMM's packed x)."""
+    :class:`PackedMatrix` (the next GEMM's packed x).  With ``residual_in`` the residual is read from
+    there and the sum stored to ``residual`` (after ``mlp.mlp_block``)."""
     device = _lib.require_gpu(partials, residual, weight, _tensor(out), name="add_partials_rms_norm")
     rows, hidden = residual.shape
     _check_out(out, rows, hidden, "add_partials_rms_norm")
-    _lib.call("oxr_add_partials_rms_norm", partials.data_ptr(), splits, rows, hidden, residual.data_ptr(),
-              weight.data_ptr(), float(eps), _tensor(out).data_ptr(), 1 if isinstance(out, PackedMatrix) else 0,
-              _lib.stream(device))
+    packed = 1 if isinstance(out, PackedMatrix) else 0
+    if residual_in is None:
+        _lib.call("oxr_add_partials_rms_norm", partials.data_ptr(), splits, rows, hidden, residual.data_ptr(),
+                  weight.data_ptr(), float(eps), _tensor(out).data_ptr(), packed, _lib.stream(device))
+    else:
+        _lib.require(tuple(residual_in.shape) == (rows, hidden) and residual_in.is_contiguous()
+                     and residual_in.dtype == torch.bfloat16, "add_partials_rms_norm: residual_in like residual")
+        _lib.call("oxr_add_partials_rms_norm_from", partials.data_ptr(), splits, rows, hidden,
+                  residual_in.data_ptr(), residual.data_ptr(), weight.data_ptr(), float(eps),
+                  _tensor(out).data_ptr(), packed, _lib.stream(device))
     return out

@@ -28,7 +28,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from . import _lib, attention, gemm, lm_head
+from . import _lib, attention, gemm, lm_head, mlp
 from .gemm import Weight
 from .kv_cache import KVCache
 
@@ -263,6 +263,13 @@ class StepBuffers:
     max_seq_len: int
     max_batch: int = field(default=0)
     pending_splits: int = field(default=0)  # partials not yet added to the residual (0: none)
+    # The one-launch MLP block (mlp.mlp_block, up to mlp.MAX_ROWS rows): its 8 output slices, the
+    # residual it writes (the next norm reads it there and stores the sum to `residual`), workspace.
+    mlp_partials: torch.Tensor | None = field(default=None)
+    residual_alt: torch.Tensor | None = field(default=None)
+    mlp_workspace: torch.Tensor | None = field(default=None)
+    pending_partials: torch.Tensor | None = field(default=None)  # the pending splits' buffer (None: partials)
+    pending_from_alt: bool = field(default=False)  # the pending residual is in residual_alt
     # Context-piece plan of the attention launches (attention.build_plan), rebuilt from the step's
     # seq_lens at the start of run_layers when `balanced` is set (contexts of different lengths).
     attn_plan: torch.Tensor | None = field(default=None)
@@ -288,6 +295,10 @@ class StepBuffers:
                                      gemm.partial_splits(config.hidden_size, config.intermediate_size)),
                                  t, config.hidden_size, dtype=torch.float32, device=device),
             max_tokens=t, max_seq_len=max_seq_len, max_batch=max_batch,
+            mlp_partials=(torch.zeros(mlp.SPLITS_OUT, t, config.hidden_size, dtype=torch.float32, device=device)
+                          if t <= mlp.MAX_ROWS else None),
+            residual_alt=torch.zeros(t, config.hidden_size, **bf) if t <= mlp.MAX_ROWS else None,
+            mlp_workspace=mlp.workspace(device) if t <= mlp.MAX_ROWS else None,
         )
 
     def enable_plan(self, config: LanguageConfig, tokens_per_seq: int) -> None:
@@ -316,6 +327,12 @@ class LanguageModel:
     def __init__(self, config: LanguageConfig, weights: LanguageWeights):
         self.config = config
         self.weights = weights.packed()
+        # gate_up with rows interleaved by 8, for the one-launch MLP block (mlp.mlp_block) where the
+        # device and shape take it; None elsewhere (the three-launch form runs).
+        self.mlp_gate_up: list[gemm.PackedMatrix] | None = None
+        if config.num_layers and mlp.supported(1, config.hidden_size, config.intermediate_size):
+            self.mlp_gate_up = [gemm.pack_weight(mlp.interleave_gate_up(layer.gate_up.unpack()))
+                                for layer in self.weights.layers]
 
     def extend(self, batch: ExtendBatch, cache: KVCache, buffers: StepBuffers | None = None) -> torch.Tensor:
         """``[B * S, hidden]``: the final-norm hidden state of every new token (language.py:201-211).
@@ -358,7 +375,7 @@ class LanguageModel:
     def embed(self, batch: ExtendBatch, buffers: StepBuffers) -> None:
         """residual = embed_tokens(ids) (decode_graph.py:164), or the caller's ``embeds``; h = layer 0's
         input norm of it."""
-        buffers.pending_splits = 0
+        buffers.pending_splits, buffers.pending_partials, buffers.pending_from_alt = 0, None, False
         c, w = self.config, self.weights
         t = batch.block_table.shape[0] * batch.tokens_per_seq
         res = buffers.residual[:t]
@@ -387,9 +404,10 @@ class LanguageModel:
         res = buffers.residual[:t]
         h = buffers.h_packed.view_rows(t) if packed else buffers.h[:t]
         if buffers.pending_splits:
-            gemm.add_partials_rms_norm(buffers.partials, buffers.pending_splits, res, weight,
-                                       self.config.rms_norm_eps, h)
-            buffers.pending_splits = 0
+            partials = buffers.partials if buffers.pending_partials is None else buffers.pending_partials
+            gemm.add_partials_rms_norm(partials, buffers.pending_splits, res, weight, self.config.rms_norm_eps, h,
+                                       residual_in=buffers.residual_alt[:t] if buffers.pending_from_alt else None)
+            buffers.pending_splits, buffers.pending_partials, buffers.pending_from_alt = 0, None, False
         else:
             self._norm(res, weight, h, stream)
 
@@ -411,6 +429,8 @@ class LanguageModel:
         if buffers.balanced and buffers.attn_plan is not None:
             plan = attention.build_plan(batch.seq_lens, s, c.num_heads, c.num_kv_heads, max_seq_len,
                                         out=buffers.attn_plan)
+        use_mlp_block = (self.mlp_gate_up is not None and buffers.mlp_workspace is not None
+                         and t <= mlp.MAX_ROWS)
         for index in range(start, stop):
             layer = w.layers[index]
             if not (first_norm_done and index == start):
@@ -423,6 +443,14 @@ class LanguageModel:
                 max_seq_len=max_seq_len, out=attn, workspace=buffers.attn_workspace, plan=plan,
             )
             buffers.pending_splits = gemm.linear_partial(attn, layer.o, buffers.partials)
+            buffers.pending_partials, buffers.pending_from_alt = None, False
+            if use_mlp_block:
+                mlp.mlp_block(buffers.partials, buffers.pending_splits, buffers.residual[:t], layer.post_norm, eps,
+                              self.mlp_gate_up[index], layer.down, buffers.residual_alt[:t], buffers.mlp_partials,
+                              buffers.mlp_workspace)
+                buffers.pending_splits, buffers.pending_partials = mlp.SPLITS_OUT, buffers.mlp_partials
+                buffers.pending_from_alt = True
+                continue
             self._settle_norm(buffers, t, layer.post_norm, stream)
             gemm.linear_silu_mul(h, layer.gate_up, out=act)
             buffers.pending_splits = gemm.linear_partial(act, layer.down, buffers.partials)
