@@ -24,11 +24,8 @@
 //   4. its 24 act columns go to the XCD's act buffer; XCD barrier; act (T x 768) into LDS,
 //   5. down: workgroup r multiplies down_proj rows [64 r, 64 r + 64) by the XCD's 768 columns of act
 //      and stores fp32 partial slice x.
-// The XCD of a workgroup is read from the hardware (HW_REG_XCC_ID); its rank among the XCD's
-// workgroups is blockIdx.x / 8, the dispatcher placing workgroups on XCDs round-robin.  Each
-// workgroup sets its rank's bit in the XCD's census word, so a placement that breaks this (two
-// workgroups of one XCD with the same rank) is reported in the error word, and every wait is
-// bounded: a barrier that cannot complete ends with an error, never a hang.
+// Placement, counters and waits: csrc/xcd_sync.h (the XCD from the hardware, rank blockIdx.x / 8, a
+// census that reports a placement breaking this, bounded waits that end with an error bit).
 //
 // Waves.  Four worker waves stream weights and multiply; a fifth, the helper, does everything that
 // waits on other workgroups (the stores that feed them, the XCD barriers, the copies into LDS).  The
@@ -45,24 +42,17 @@
 // the workers issue the weight ring only once the helper has requested that copy.  Requesting the
 // ring earlier (before or right after the norm) delayed the norm's stores or the copy behind it by
 // 3-5 us and made the block no faster.
-// Counters.  Per XCD: census bits, norm rows done, act chunks done, workgroups finished.  The last
-// workgroup of an XCD to finish zeroes its XCD's words (every other one has passed its last wait),
-// so a launch leaves them as it found them.  Synchronisation inside an XCD: plain stores, a wait for
-// their completion, then an atomic add on the XCD's counter; waiters poll with sc1 loads and read
-// the data with sc0 loads (L1 bypassed); measured exact on MI355X.
-#include "common.h"
+#include "xcd_sync.h"
 
 namespace oxr {
 namespace {
 
-constexpr int kXcds = 8;
-constexpr int kXcdWgs = 32;  // workgroups per XCD: one per CU
-constexpr int kGrid = kXcds * kXcdWgs;
+using namespace xcd;
+
 constexpr int kWorkers = 4;
 constexpr int kThreads = 64 * (kWorkers + 1);
 constexpr int kMaxRows = 32;
 constexpr int kRing = 8;  // 128-k weight steps in flight per worker wave (4 KiB each)
-constexpr uint32_t kSpinLimit = 1u << 16;
 
 // Block shape: the config-5 decoder (hidden 2048, intermediate 6144).
 constexpr int kH = 2048, kI = 6144;
@@ -76,16 +66,10 @@ constexpr int kSteps = kGSteps + kDSteps;       // 18
 static_assert(kH / 16 / kXcdWgs == kWorkers, "one down_proj row tile per worker");
 static_assert(kIw % 8 == 0 && kIx % 128 == 0 && kH % (128 * kWorkers) == 0, "block shape");
 
-// Control words (uint32) at the workspace start: one 256-byte block per XCD, then the error word.
-constexpr int kCtlStride = 64;
-enum Ctl { kCensus = 0, kNormDone = 1, kActDone = 2, kExit = 3 };
-constexpr int kErrorWord = kXcds * kCtlStride;
-constexpr size_t kCtlBytes = 4096;
+enum MlpCtl { kNormDone = kPhase0, kActDone = kPhase1 };
 constexpr size_t kHElems = (size_t)kMaxRows * kH;      // one XCD's copy of h, packed
 constexpr size_t kActElems = (size_t)kMaxRows * kIx;   // one XCD's act slice, packed
 constexpr size_t kWorkspaceBytes = kCtlBytes + kXcds * (kHElems + kActElems) * sizeof(bf16_t);
-
-enum Error : uint32_t { kErrPlacement = 1, kErrNormWait = 2, kErrActWait = 4 };
 
 struct MlpArgs {
   const float* o_part;    // [o_splits][rows][kH]
@@ -102,60 +86,6 @@ struct MlpArgs {
   bf16_t* h_x;            // [kXcds][kHElems]
   bf16_t* act_x;          // [kXcds][kActElems]
 };
-
-__device__ __forceinline__ uint32_t xcc_id() {
-  uint32_t v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  return v & 0xfu;
-}
-
-// A counter read that sees the XCD's L2 atomics (sc1; an sc0 poll was measured to return a stale
-// value after an atomic to another line).
-__device__ __forceinline__ uint32_t load_sc1(const uint32_t* p) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, 4, 0x00020000);
-  return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 16);
-}
-
-__device__ __forceinline__ uint32_t atomic_add(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void set_error(uint32_t* ctl, uint32_t bits) {
-  __hip_atomic_fetch_or(ctl + kErrorWord, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// Wait (helper wave) until *ctr >= target; false after kSpinLimit polls.
-__device__ __forceinline__ bool wait_count(const uint32_t* ctr, uint32_t target) {
-  for (uint32_t n = 0; n < kSpinLimit; ++n) {
-    if (__builtin_amdgcn_readfirstlane(load_sc1(ctr)) >= target) return true;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  return false;
-}
-
-// All of this wave's stores have completed (are in L2) before what follows.
-__device__ __forceinline__ void stores_done() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Count this workgroup into an XCD counter (lane 0), then wait until the atomic has been performed
-// (an atomic without return still holds the vector memory counter until it is acknowledged).
-__device__ __forceinline__ void arrive(uint32_t* ctr, int lane) {
-  if (lane == 0) atomic_add(ctr, 1u);
-  stores_done();
-}
-
-__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// 1 KiB blocks [0, n) of a packed buffer into LDS at the same offsets, L1 bypassed (sc0): lane i of a
-// block writes its bytes [16 i, 16 i + 16).
-__device__ __forceinline__ void copy_to_lds(const bf16_t* src, bf16_t* dst, int n, int lane) {
-  for (int j = 0; j < n; ++j)
-    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src + j * 512 + lane * 8),
-                                     (void __attribute__((address_space(3)))*)(dst + j * 512), 16, 0, 1);
-}
 
 template <int NB, int P>
 __global__ __launch_bounds__(kThreads) void mlp_block_kernel(MlpArgs a) {
@@ -179,10 +109,7 @@ __global__ __launch_bounds__(kThreads) void mlp_block_kernel(MlpArgs a) {
 
   if (wave == kWorkers) {
     // ---------------------------------------------------------------- helper wave
-    if (lane == 0) {
-      const uint32_t seen = __hip_atomic_fetch_or(ctl + kCensus, 1u << rank, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (((seen >> rank) & 1u) || xcc >= (uint32_t)kXcds) set_error(a.ctl, kErrPlacement);
-    }
+    census(a.ctl, ctl, rank, xcc, lane);
     barrier();  // S1: the workers' norm sums
     barrier();  // S2: the norm row in LDS
     if (has_row) {
@@ -195,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void mlp_block_kernel(MlpArgs a) {
       stores_done();
       arrive(ctl + kNormDone, lane);
     }
-    if (!wait_count(ctl + kNormDone, (uint32_t)rows) && lane == 0) set_error(a.ctl, kErrNormWait);
+    if (!wait_count(ctl + kNormDone, (uint32_t)rows) && lane == 0) set_error(a.ctl, kErrPhase0Wait);
     copy_to_lds(h_x, lx, NB * 16 * kH / 512, lane);
     barrier();  // S3: copy requested
     stores_done();
@@ -209,17 +136,11 @@ __global__ __launch_bounds__(kThreads) void mlp_block_kernel(MlpArgs a) {
     }
     stores_done();
     arrive(ctl + kActDone, lane);
-    if (!wait_count(ctl + kActDone, (uint32_t)kXcdWgs) && lane == 0) set_error(a.ctl, kErrActWait);
+    if (!wait_count(ctl + kActDone, (uint32_t)kXcdWgs) && lane == 0) set_error(a.ctl, kErrPhase1Wait);
     copy_to_lds(act_x, lx, NB * 16 * kIx / 512, lane);
     stores_done();
     barrier();  // S7: act in LDS
-    if (lane == 0 && atomic_add(ctl + kExit, 1u) == (uint32_t)(kXcdWgs - 1)) {
-      // Last workgroup of this XCD: every other one has passed its last wait.
-      ctl[kCensus] = 0u;
-      ctl[kNormDone] = 0u;
-      ctl[kActDone] = 0u;
-      ctl[kExit] = 0u;
-    }
+    finish(ctl, lane);
     return;
   }
 
@@ -394,20 +315,6 @@ int launch_nb(const MlpArgs& a, hipStream_t s) {
   else
     hipLaunchKernelGGL((mlp_block_kernel<NB, 8>), dim3(kGrid), dim3(kThreads), 0, s, a);
   return OXR_LAUNCH_STATUS();
-}
-
-// The block's layout assumes an MI355X in its default single-partition mode: 256 CUs in 8 XCDs.
-bool device_fits() {
-  static int cached = -1;
-  if (cached < 0) {
-    int dev = 0, cus = 0;
-    cached = hipGetDevice(&dev) == hipSuccess &&
-                     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-                     cus == kGrid
-                 ? 1
-                 : 0;
-  }
-  return cached == 1;
 }
 
 }  // namespace
