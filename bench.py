@@ -127,8 +127,8 @@ def time_attention(config, model, cache, loop, context: torch.Tensor, iters: int
             cache.k[i % c.num_layers], cache.v[i % c.num_layers], slots, seq, loop.block_table, c.num_heads,
             scale=c.head_dim ** -0.5, max_seq_len=max_seq_len, out=out, workspace=ws, plan=plan)
 
-    for i in range(c.num_layers):
-        run(i)
+    calls = iter(range(1 << 62))
+    _spin_up(lambda: run(next(calls)))
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -148,6 +148,26 @@ COPY_BYTES = 256 << 20  # calibration copy for the FETCH_SIZE / WRITE_SIZE count
 TRAFFIC_FILE = ROOT / "profiles" / "paged_extend_traffic.md"
 
 
+SPIN_UP_S = 0.25  # untimed work before each timed region below
+
+
+def _spin_up(fn, seconds: float = SPIN_UP_S) -> None:
+    """Call ``fn`` (one untimed launch or graph replay) until ``seconds`` of wall time have passed, and
+    at least three times.  An MI355X that has been idle for a moment runs its next launches at a lower
+    shader clock and needs about a tenth of a second of steady load to reach its running clock
+    (measured: one 8 x 4096 causal prefill launch 758 us after 3 s idle, 622 us under steady load), so
+    a timed region of a few milliseconds right after host-side set-up would time the ramp."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while n < 3 or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
     """The one-token decode step (``DecodeGraphs``, decode_graph.py:33-119) for the same B sequences
     at their current context: one new token each, graph replays with the inputs already on the
@@ -162,8 +182,7 @@ def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
     tables = [table[i, : (p + 1 + bs - 1) // bs].tolist() for i, p in enumerate(positions)]
     graphs.run([1] * b, positions, slots, (seq + 1).tolist(), tables)
     graph = graphs.graph(graphs.buckets[-1])
-    for _ in range(3):
-        graph.replay()
+    _spin_up(graph.replay)
     stream = torch.cuda.current_stream()  # where replay() launches the graph
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -192,8 +211,7 @@ def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, see
     v = torch.randn(t, kv, d, generator=g, device="cuda").to(torch.bfloat16)
     cu = torch.arange(0, t + 1, length, dtype=torch.int32, device="cuda")
     out = torch.empty_like(q)
-    for _ in range(3):
-        attention.varlen(q, k, v, cu, length, causal=causal, out=out)
+    _spin_up(lambda: attention.varlen(q, k, v, cu, length, causal=causal, out=out))
     stream = torch.cuda.current_stream()  # where the wrapper launches
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -226,7 +244,7 @@ def _time_us(fn, iters: int = 20, per_graph: int = 10) -> float:
         for _ in range(per_graph):
             fn()
     torch.cuda.synchronize()
-    graph.replay()
+    _spin_up(graph.replay)
     stream = torch.cuda.current_stream()  # where replay() launches the graph
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()

@@ -35,6 +35,9 @@
 // Causal prefill runs this 4-wave kernel.  Bidirectional prefill runs the
 // 8-wave ping-pong kernel further down (same tiles and products, its two wave
 // groups alternating softmax and MFMA phases on each SIMD).
+#include <algorithm>
+#include <atomic>
+
 #include "common.h"
 
 namespace oxr {
@@ -47,6 +50,20 @@ constexpr int kVWaves = 4;             // waves per workgroup
 constexpr int kVRows = 32 * kVWaves;   // query rows per workgroup (all q heads of the kv head)
 constexpr int kKeyTile = 64;           // keys per LDS stage
 constexpr int kLoadsPerWave = kKeyTile * kVD * 2 / 1024 / kVWaves;  // 1 KiB direct-to-LDS loads per wave and tensor
+constexpr int kPersistentSlots = 64;   // persistent causal launch: workgroups per XCD (two per CU)
+
+// Work counters of the persistent causal launch, per launch slot (the host cycles through
+// kSchedRing of them, so launches in flight at once on different streams use different counters)
+// and per XCD group: word 0 is the next item to hand out, word 32 the workgroups that have finished.
+// The group's last workgroup to finish zeroes both, so every launch finds them at zero (they are
+// zero when the module loads).  System-scope atomics: performed coherently for the whole device.
+constexpr int kSchedRing = 16;
+constexpr int kSchedStride = 64;  // uint32 words per (launch slot, XCD group)
+__device__ uint32_t g_varlen_sched[kSchedRing * 8 * kSchedStride];
+
+__device__ __forceinline__ uint32_t sched_take(uint32_t* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 __device__ __forceinline__ f32x16 mfma_32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
@@ -77,30 +94,25 @@ __device__ __forceinline__ float row_max32(const f32x16 (&sv)[2]) {
   return fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
 }
 
+// One work item: query tile `qt` (128 / G positions of each of the G q heads) of (sequence, kv head)
+// pair `pair`.  Every wave of the workgroup takes part (it ends with a workgroup barrier and touches no
+// LDS after it, so the next item may start right away).  With a counter `ctr`, thread 0 takes the next
+// item number from it into `next` when the item's last two key tiles begin (or at once if it has no
+// work), late enough that the items are started in list order.
 template <bool kCausal>
-__global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const int32_t* __restrict__ cu_seqlens, int H, int KV, int num_qtiles, float scale_log2,
-    bf16_t* __restrict__ out) {
-  // Two buffers per tensor, as separate arrays: the loop below is unrolled by two, so each buffer is
-  // named statically and the compiler can tell a prefetch into one from reads of the other.
-  __shared__ bf16_t s_k0[kKeyTile * kVD], s_k1[kKeyTile * kVD];
-  __shared__ bf16_t s_v0[kKeyTile * kVD], s_v1[kKeyTile * kVD];
-
-  // Workgroup b runs on XCD b % 8 (round-robin dispatch).  XCD x takes the x-th eighth of the
-  // work items, in order, so the query tiles resident on one XCD at a time belong to one or two
-  // (sequence, kv head) pairs and share that pair's key tiles in the XCD's L2.  Item w is query
-  // tile w % num_qtiles (late tiles first) of pair w / num_qtiles.
-  const int total = (int)gridDim.x, xcd = (int)blockIdx.x & 7, slot = (int)blockIdx.x >> 3;
-  const int w = xcd * (total >> 3) + min(xcd, total & 7) + slot;
-  const int pair = w / num_qtiles;
+__device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                            const bf16_t* __restrict__ v, const int32_t* __restrict__ cu_seqlens,
+                                            int H, int KV, float scale_log2, bf16_t* __restrict__ out, int pair,
+                                            int qt, bf16_t* s_k0, bf16_t* s_k1, bf16_t* s_v0, bf16_t* s_v1,
+                                            uint32_t* ctr = nullptr, int* next = nullptr) {
   const int seq = pair / KV, kvh = pair - seq * KV;
   const int start = cu_seqlens[seq], len = cu_seqlens[seq + 1] - start;
   const int G = H / KV, rph = kVRows / G;  // positions per head in this workgroup
-  // Query tiles in reverse order: under the causal mask the late ones do the most work, so they
-  // are dispatched first.
-  const int q0 = (num_qtiles - 1 - (w - pair * num_qtiles)) * rph;  // first position, per head
-  if (q0 >= len) return;                                    // whole workgroup: before any barrier
+  const int q0 = qt * rph;                 // first position, per head
+  if (q0 >= len) {                         // whole workgroup: before any barrier
+    if (ctr != nullptr && threadIdx.x == 0) *next = (int)sched_take(ctr);
+    return;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -264,6 +276,7 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   __syncthreads();
   qk(s_k0, sa);
   for (int t = 0; t < tiles; t += 2) {
+    if (ctr != nullptr && t + 2 >= tiles && threadIdx.x == 0) *next = (int)sched_take(ctr);
     step(t, sa, sb, s_k1, s_v0, s_k0, s_v1);
     if (t + 1 < tiles) step(t + 1, sb, sa, s_k0, s_v1, s_k1, s_v0);
   }
@@ -280,6 +293,61 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
         *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * m) =
             u32x2{pack_bf(o[dt][4 * m] * inv, o[dt][4 * m + 1] * inv),
                   pack_bf(o[dt][4 * m + 2] * inv, o[dt][4 * m + 3] * inv)};
+  }
+}
+
+// kPersistent = false: one work item per workgroup.  Workgroup b runs on XCD b % 8 (round-robin
+// dispatch); XCD x takes the x-th eighth of the items in order, so the query tiles resident on one XCD
+// at a time belong to one or two (sequence, kv head) pairs and share that pair's key tiles in the
+// XCD's L2.  Item w is query tile w % num_qtiles (late tiles first: under the causal mask they do the
+// most work) of pair w / num_qtiles.
+// kPersistent = true (pairs divisible by 8): 64 workgroups per XCD (two per CU) take items from their
+// XCD group's list through a shared counter until it runs out, so no CU waits for the dispatcher
+// between items, and a workgroup that runs slower (measured: of two equal workgroups on one CU the
+// younger one took 24% longer) takes fewer items.  XCD group x owns pairs [x P, x P + P),
+// P = pairs / 8, listed two pairs at a time (their key tiles fit the XCD's L2), each two's query tiles
+// latest first, so the list ends with the smallest items.  A workgroup asks for its next item near
+// the end of its current one and reads the answer after the item's last barrier.
+template <bool kCausal, bool kPersistent>
+__global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const int32_t* __restrict__ cu_seqlens, int H, int KV, int num_qtiles, int num_pairs, int ring,
+    float scale_log2, bf16_t* __restrict__ out) {
+  // Two buffers per tensor, as separate arrays: the tile loop is unrolled by two, so each buffer is
+  // named statically and the compiler can tell a prefetch into one from reads of the other (members
+  // of one array or struct, addressed per wave, it cannot: it then waits for every prefetch before
+  // each tile's first LDS read).
+  __shared__ bf16_t s_k0[kKeyTile * kVD], s_k1[kKeyTile * kVD];
+  __shared__ bf16_t s_v0[kKeyTile * kVD], s_v1[kKeyTile * kVD];
+  const int total = (int)gridDim.x, xcd = (int)blockIdx.x & 7, slot = (int)blockIdx.x >> 3;
+  if constexpr (!kPersistent) {
+    const int w = xcd * (total >> 3) + min(xcd, total & 7) + slot;
+    const int pair = w / num_qtiles;
+    varlen_item<kCausal>(q, k, v, cu_seqlens, H, KV, scale_log2, out, pair,
+                         num_qtiles - 1 - (w - pair * num_qtiles), s_k0, s_k1, s_v0, s_v1);
+  } else {
+    // Item numbers pass through LDS, alternating between two words: a word is rewritten two items
+    // later, after a barrier that every wave reaches only once it has read the word.
+    __shared__ int s_item[2];
+    uint32_t* const ctr = g_varlen_sched + (ring * 8 + xcd) * kSchedStride;
+    const int P = num_pairs >> 3, items = P * num_qtiles;
+    if (threadIdx.x == 0) s_item[0] = (int)sched_take(ctr);
+    __syncthreads();
+    int i = s_item[0];
+    for (int r = 1; i < items; ++r) {
+      int next = 0;
+      const int g = i / (2 * num_qtiles), gp = min(2, P - 2 * g), j = i - g * 2 * num_qtiles;
+      varlen_item<kCausal>(q, k, v, cu_seqlens, H, KV, scale_log2, out, xcd * P + 2 * g + j % gp,
+                           num_qtiles - 1 - j / gp, s_k0, s_k1, s_v0, s_v1, ctr, &next);
+      if (threadIdx.x == 0) s_item[r & 1] = next;
+      __syncthreads();
+      i = s_item[r & 1];
+    }
+    // Every workgroup of the group has taken its last number once all have counted themselves out.
+    if (threadIdx.x == 0 && sched_take(ctr + 32) == (uint32_t)(total / 8 - 1)) {
+      __hip_atomic_exchange(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_exchange(ctr + 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 }
 
@@ -566,14 +634,23 @@ extern "C" int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const 
   const dim3 grid((unsigned)(num_qtiles * num_kv_heads * num_seqs));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
-  if (pingpong)
+  const int num_pairs = num_seqs * num_kv_heads;
+  static std::atomic<uint32_t> launches{0};
+  if (pingpong) {
     hipLaunchKernelGGL(varlen_attention_pp_kernel<false>, grid, dim3(64 * kPWaves), 0, s, q, k, v, cu_seqlens,
                        num_heads, num_kv_heads, num_qtiles, scale_log2, out);
-  else if (causal)
-    hipLaunchKernelGGL(varlen_attention_kernel<true>, grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
-                       num_heads, num_kv_heads, num_qtiles, scale_log2, out);
-  else
-    hipLaunchKernelGGL(varlen_attention_kernel<false>, grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
-                       num_heads, num_kv_heads, num_qtiles, scale_log2, out);
+  } else if (causal && num_pairs % 8 == 0) {
+    // Persistent: two workgroups per CU of the 256, or fewer when an XCD has fewer items.
+    const int per_xcd = (int)std::min<int64_t>(kPersistentSlots, (int64_t)(num_pairs / 8) * num_qtiles);
+    const int ring = (int)(launches.fetch_add(1u, std::memory_order_relaxed) % kSchedRing);
+    hipLaunchKernelGGL((varlen_attention_kernel<true, true>), dim3(8 * per_xcd), dim3(64 * kVWaves), 0, s, q, k, v,
+                       cu_seqlens, num_heads, num_kv_heads, num_qtiles, num_pairs, ring, scale_log2, out);
+  } else if (causal) {
+    hipLaunchKernelGGL((varlen_attention_kernel<true, false>), grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
+                       num_heads, num_kv_heads, num_qtiles, num_pairs, 0, scale_log2, out);
+  } else {
+    hipLaunchKernelGGL((varlen_attention_kernel<false, false>), grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
+                       num_heads, num_kv_heads, num_qtiles, num_pairs, 0, scale_log2, out);
+  }
   return OXR_LAUNCH_STATUS();
 }

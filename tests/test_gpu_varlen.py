@@ -3,7 +3,8 @@
 ``attention.varlen`` is the drop-in for attention.varlen (oxr_runtime/attention.py:47-59).  Cases:
 lengths around the 16-row query and 64-key tile edges, an empty sequence, one-token sequences,
 causal and bidirectional, every supported head grouping (1, 2, 4 and 8 q heads per kv head),
-and prefill-sized sequences.
+prefill-sized sequences, and the persistent causal launch (pairs divisible by 8) over several
+rounds of items per workgroup.
 """
 
 from __future__ import annotations
@@ -58,6 +59,14 @@ def test_head_groupings(kv, causal) -> None:
 @pytest.mark.parametrize("causal", [True, False])
 def test_prefill_sizes(causal) -> None:
     _case([1024, 777], 16, 8, causal, seed=20 + causal)
+
+
+@pytest.mark.parametrize("lens", [[700, 513, 1, 0, 640, 64, 300, 129], [1500, 900, 5]])
+def test_persistent_rounds(lens) -> None:
+    # 32 q heads over 8 kv heads: pairs divisible by 8 take the persistent causal launch, here with
+    # several rounds of items per workgroup, ragged and empty sequences, and (3 sequences: 3 pairs
+    # per XCD) a last pair group of one.
+    _case(lens, 32, 8, True, seed=30 + len(lens))
 
 
 def test_rejects_unsupported_grouping() -> None:
