@@ -4,7 +4,7 @@
 lengths around the 16-row query and 64-key tile edges, an empty sequence, one-token sequences,
 causal and bidirectional, every supported head grouping (1, 2, 4 and 8 q heads per kv head),
 prefill-sized sequences, and the persistent causal launch (pairs divisible by 8) over several
-rounds of items per workgroup.
+rounds of items per workgroup, replayed from a captured graph and run on two streams at once.
 """
 
 from __future__ import annotations
@@ -67,6 +67,69 @@ def test_persistent_rounds(lens) -> None:
     # several rounds of items per workgroup, ragged and empty sequences, and (3 sequences: 3 pairs
     # per XCD) a last pair group of one.
     _case(lens, 32, 8, True, seed=30 + len(lens))
+
+
+def _inputs(lens, H, KV, seed):
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q, k, v = (torch.randn(T, n, 128, generator=g, device="cuda").to(torch.bfloat16) for n in (H, KV, KV))
+    return q, k, v, torch.from_numpy(cu).cuda()
+
+
+def test_persistent_graph_replays() -> None:
+    # The persistent launch's work counters reset themselves at the end of each launch, so a captured
+    # launch replays correctly; eager launches (other inputs) run between the replays.  Items are
+    # independent of the workgroup that computes them, so every result is bit-identical.
+    lens = [640, 1, 300, 513, 0, 64, 700, 129]
+    q, k, v, cu = _inputs(lens, 32, 8, seed=41)
+    q2, k2, v2, cu2 = _inputs([97, 1500, 33, 5, 800, 2, 64, 257], 32, 8, seed=42)
+    announce("varlen graph replays", lens)
+    want = attention.varlen(q, k, v, cu, max(lens), causal=True)
+    want2 = attention.varlen(q2, k2, v2, cu2, 1500, causal=True)
+    out = torch.full_like(q, float("nan"))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        attention.varlen(q, k, v, cu, max(lens), causal=True, out=out)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits_t(out), _bits_t(want))
+        got2 = attention.varlen(q2, k2, v2, cu2, 1500, causal=True)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits_t(got2), _bits_t(want2))
+
+
+def test_persistent_concurrent_streams() -> None:
+    # Two persistent launches in flight at once on two streams use different counter sets.
+    a = _inputs([1024, 700, 3, 900, 1024, 0, 512, 64], 32, 8, seed=43)
+    b = _inputs([800] * 8, 32, 8, seed=44)
+    announce("varlen concurrent streams")
+    want_a = attention.varlen(*a[:4], 1024, causal=True)
+    want_b = attention.varlen(*b[:4], 800, causal=True)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for _ in range(4):
+        with torch.cuda.stream(s1):
+            oa = attention.varlen(*a[:4], 1024, causal=True)
+        with torch.cuda.stream(s2):
+            ob = attention.varlen(*b[:4], 800, causal=True)
+        outs.append((oa, ob))
+    torch.cuda.synchronize()
+    for oa, ob in outs:
+        assert torch.equal(_bits_t(oa), _bits_t(want_a))
+        assert torch.equal(_bits_t(ob), _bits_t(want_b))
+
+
+def _bits_t(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().view(torch.int16)
 
 
 def test_rejects_unsupported_grouping() -> None:
