@@ -199,34 +199,45 @@ def time_decode(config, model, cache, loop, iters: int = 50) -> dict:
             "achieved_gbs": traffic / (us * 1e-6) / 1e9}
 
 
-def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, seed: int = 0, causal: bool = True) -> dict:
+def time_prefill(config, seqs: int = 8, length: int = 4096, iters: int = 10, seed: int = 0, causal: bool = True,
+                 lens: list[int] | None = None) -> dict:
     """Prefill attention (``attention.varlen``, the drop-in for attention.py:47-59): causal or
-    bidirectional over ``seqs`` sequences of ``length`` tokens at the model's head shape, inputs
-    resident on the device.  Flops = 4 * head_dim * heads * (query-key pairs attended)."""
+    bidirectional over ``seqs`` sequences of ``length`` tokens (or of the given ``lens``) at the model's
+    head shape, inputs resident on the device.  Flops = 4 * head_dim * heads * (query-key pairs
+    attended)."""
     h, kv, d = config.num_heads, config.num_kv_heads, config.head_dim
-    t = seqs * length
+    lens = [length] * seqs if lens is None else [int(n) for n in lens]
+    cu_np = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    t, max_len = int(cu_np[-1]), max(lens)
     g = torch.Generator(device="cuda").manual_seed(seed)
     q = torch.randn(t, h, d, generator=g, device="cuda").to(torch.bfloat16)
     k = torch.randn(t, kv, d, generator=g, device="cuda").to(torch.bfloat16)
     v = torch.randn(t, kv, d, generator=g, device="cuda").to(torch.bfloat16)
-    cu = torch.arange(0, t + 1, length, dtype=torch.int32, device="cuda")
+    cu = torch.from_numpy(cu_np).to("cuda")
     out = torch.empty_like(q)
-    _spin_up(lambda: attention.varlen(q, k, v, cu, length, causal=causal, out=out))
+    _spin_up(lambda: attention.varlen(q, k, v, cu, max_len, causal=causal, out=out))
     stream = torch.cuda.current_stream()  # where the wrapper launches
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
     for _ in range(iters):
-        attention.varlen(q, k, v, cu, length, causal=causal, out=out)
+        attention.varlen(q, k, v, cu, max_len, causal=causal, out=out)
     end.record(stream)
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1000.0 / iters
-    flops = 4.0 * d * h * seqs * (length * (length + 1) / 2 if causal else length * length)
+    flops = sum(4.0 * d * h * (n * (n + 1) / 2 if causal else n * n) for n in lens)
     tflops = flops / (us * 1e-6) / 1e12
     del q, k, v, out
-    return {"workload": f"varlen {'causal' if causal else 'bidirectional'}, {seqs} x {length} tokens, {h}/{kv} heads, head_dim {d}", "us": us,
+    shape = (f"{len(lens)} x {length} tokens" if len(set(lens)) == 1 else
+             f"{len(lens)} sequences, lengths {min(lens)}..{max(lens)} ({t} tokens)")
+    return {"workload": f"varlen {'causal' if causal else 'bidirectional'}, {shape}, {h}/{kv} heads, head_dim {d}", "us": us,
             "flops": flops, "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
+
+
+def ragged_lengths(seed: int = 0, seqs: int = 32, longest: int = 4096) -> list[int]:
+    """A prefill batch of mixed prompt lengths: ``seqs`` lengths uniform in [1, longest]."""
+    return np.random.default_rng(seed).integers(1, longest + 1, seqs).tolist()
 
 
 def _time_us(fn, iters: int = 20, per_graph: int = 10) -> float:
@@ -577,6 +588,7 @@ def main() -> int:
     if args.prefill_driver:
         print(json.dumps(time_prefill(language.QWEN_SYNTHETIC)), flush=True)
         print(json.dumps(time_prefill(language.QWEN_SYNTHETIC, causal=False)), flush=True)
+        print(json.dumps(time_prefill(language.QWEN_SYNTHETIC, lens=ragged_lengths(args.seed))), flush=True)
         return 0
     if args.configs_driver:
         c = language.QWEN_SYNTHETIC
@@ -636,7 +648,9 @@ def main() -> int:
     log(f"decode step (B={decode['batch']}, one token each) {decode['step_us']:.1f} us")
     prefill = time_prefill(config)
     prefill_bidir = time_prefill(config, causal=False)
-    log(f"prefill attention {prefill['us']:.1f} us, {prefill['achieved']:.0f} TFLOP/s")
+    prefill_ragged = time_prefill(config, lens=ragged_lengths(args.seed))
+    log(f"prefill attention {prefill['us']:.1f} us, {prefill['achieved']:.0f} TFLOP/s; mixed lengths "
+        f"{prefill_ragged['us']:.1f} us, {prefill_ragged['achieved']:.0f} TFLOP/s")
     configs = time_configs(config, model.weights.lm_head, args.seed)
     log("configs: " + json.dumps(configs))
 
@@ -683,6 +697,7 @@ def main() -> int:
                         "frac": decode["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill_attention": prefill,
         "prefill_attention_bidirectional": prefill_bidir,
+        "prefill_attention_mixed_lengths": prefill_ragged,
         "configs": configs,
         "cpu_baseline": cpu,
         "wall_s_timed": wall,
