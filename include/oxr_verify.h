@@ -434,9 +434,9 @@ int oxr_argmax(const void* logits, int32_t dtype, int64_t rows, int64_t vocab, i
  * attends keys [0, j] when causal != 0, else all keys, of kv head
  * h / (num_heads / num_kv_heads); scores q.k * scale, fp32 softmax, output
  * bf16 [T, num_heads, 128].  num_heads / num_kv_heads must be 1, 2, 4 or 8.
- * Causal launches with num_seqs * num_kv_heads divisible by 8 hand out work
- * through counters in the library's static device memory, one of 16 sets per
- * launch in turn: at most 16 such launches may run at once on one device.
+ * Causal launches hand out work through counters in the library's static
+ * device memory, one of 16 sets per launch in turn: at most 16 causal launches
+ * may run at once on one device.
  */
 int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const oxr_bf16* v, const int32_t* cu_seqlens,
                          int32_t num_seqs, int32_t max_len, int32_t num_heads, int32_t num_kv_heads,

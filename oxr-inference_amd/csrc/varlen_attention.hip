@@ -32,9 +32,10 @@
 //   wave overlap.
 // * Causal: key tiles above a wave's last row are skipped, tiles that cross a
 //   row's diagonal are masked per element; keys past the sequence are masked.
-// Causal prefill runs this 4-wave kernel.  Bidirectional prefill runs the
-// 8-wave ping-pong kernel further down (same tiles and products, its two wave
-// groups alternating softmax and MFMA phases on each SIMD).
+// Causal prefill runs this 4-wave kernel as a persistent launch whose
+// workgroups take query tiles from shared lists.  Bidirectional prefill runs
+// the 8-wave ping-pong kernel further down (same tiles and products, its two
+// wave groups alternating softmax and MFMA phases on each SIMD).
 #include <algorithm>
 #include <atomic>
 
@@ -298,21 +299,17 @@ __device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const 
   }
 }
 
-// kPersistent = false: one work item per workgroup.  Workgroup b runs on XCD b % 8 (round-robin
-// dispatch); XCD x takes the x-th eighth of the items in order, so the query tiles resident on one XCD
-// at a time belong to one or two (sequence, kv head) pairs and share that pair's key tiles in the
-// XCD's L2.  Item w is query tile w % num_qtiles (late tiles first: under the causal mask they do the
-// most work) of pair w / num_qtiles.
-// kPersistent = true (pairs divisible by 8): 64 workgroups per XCD (two per CU) take items from their
-// XCD group's list through a shared counter until it runs out, so no CU waits for the dispatcher
-// between items, and a workgroup that runs slower (measured: of two equal workgroups on one CU the
-// younger one took 24% longer) takes fewer items.  XCD group x owns pairs [x P, x P + P),
-// P = pairs / 8, listed two pairs at a time (their key tiles fit the XCD's L2), each two's query tiles
-// latest first, so the list ends with the smallest items.  A workgroup asks for its next item near
-// the end of its current one and reads the answer after the item's last barrier.  Once its group's list
-// is done it takes the remaining items of the other groups' lists, in turn (measured: with each XCD
-// on its own list alone, the XCDs' mean end times spread from 646 to 694 us in a 705 us launch).
-template <bool kCausal, bool kPersistent>
+// Causal prefill, persistent: 64 workgroups per XCD (two per CU) take items from lists through shared
+// counters until every list runs out, so no CU waits for the dispatcher between items, and a workgroup
+// that runs slower (measured: of two equal workgroups on one CU the younger one took 24% longer) takes
+// fewer items.  XCD group x owns pairs [x n / 8, (x + 1) n / 8) of the n (sequence, kv head) pairs,
+// listed two pairs at a time (their key tiles fit the XCD's L2), each two's query tiles latest first,
+// so a list ends with its smallest items.  A workgroup starts on its own XCD's group (workgroup b runs
+// on XCD b % 8, round-robin dispatch), asks for its next item near the end of its current one and
+// reads the answer after the item's last barrier; once that list is done it takes the remaining items
+// of the other groups' lists, in turn.  That balances the XCDs (measured: alone on their own lists,
+// their mean end times spread from 646 to 694 us in a 705 us launch) and mixed sequence lengths, whose
+// long sequences' pairs sit in few groups.
 __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const int32_t* __restrict__ cu_seqlens, int H, int KV, int num_qtiles, int num_pairs, int ring,
@@ -323,48 +320,48 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
   // each tile's first LDS read).
   __shared__ bf16_t s_k0[kKeyTile * kVD], s_k1[kKeyTile * kVD];
   __shared__ bf16_t s_v0[kKeyTile * kVD], s_v1[kKeyTile * kVD];
-  const int total = (int)gridDim.x, xcd = (int)blockIdx.x & 7, slot = (int)blockIdx.x >> 3;
-  if constexpr (!kPersistent) {
-    const int w = xcd * (total >> 3) + min(xcd, total & 7) + slot;
-    const int pair = w / num_qtiles;
-    varlen_item<kCausal>(q, k, v, cu_seqlens, H, KV, scale_log2, out, pair,
-                         num_qtiles - 1 - (w - pair * num_qtiles), s_k0, s_k1, s_v0, s_v1);
-  } else {
-    // Item numbers pass through LDS, alternating between two words: a word is rewritten two numbers
-    // later, after a barrier that every wave reaches only once it has read the word.
-    __shared__ int s_item[2];
-    uint32_t* const base = g_varlen_sched + ring * kSchedWords;
-    const int P = num_pairs >> 3, items = P * num_qtiles;
-    int grp = xcd, tried = 0, r = 0;
-    if (threadIdx.x == 0) s_item[0] = (int)sched_take(base + grp * kSchedStride);
-    __syncthreads();
-    int i = s_item[0];
-    while (true) {
-      if (i >= items) {
-        // This group's list is done: take from the next group's (XCDs do not run at the same speed;
-        // the lists end with their smallest items).
-        if (++tried == 8) break;
-        grp = (grp + 1) & 7;
-        ++r;
-        if (threadIdx.x == 0) s_item[r & 1] = (int)sched_take(base + grp * kSchedStride);
-        __syncthreads();
-        i = s_item[r & 1];
-        continue;
-      }
-      int next = 0;
-      const int g = i / (2 * num_qtiles), gp = min(2, P - 2 * g), j = i - g * 2 * num_qtiles;
-      varlen_item<kCausal>(q, k, v, cu_seqlens, H, KV, scale_log2, out, grp * P + 2 * g + j % gp,
-                           num_qtiles - 1 - j / gp, s_k0, s_k1, s_v0, s_v1, base + grp * kSchedStride, &next);
+  // Item numbers pass through LDS, alternating between two words: a word is rewritten two numbers
+  // later, after a barrier that every wave reaches only once it has read the word.
+  __shared__ int s_item[2];
+  const int total = (int)gridDim.x;
+  uint32_t* const base = g_varlen_sched + ring * kSchedWords;
+  int grp = (int)blockIdx.x & 7, tried = 0, r = 0;
+  // Group grp's pairs [lo, lo + cnt) and list length.
+  int lo = 0, cnt = 0, items = 0;
+  auto group = [&]() {
+    lo = (int)((int64_t)grp * num_pairs / 8);
+    cnt = (int)((int64_t)(grp + 1) * num_pairs / 8) - lo;
+    items = cnt * num_qtiles;
+  };
+  group();
+  if (threadIdx.x == 0) s_item[0] = (int)sched_take(base + grp * kSchedStride);
+  __syncthreads();
+  int i = s_item[0];
+  while (true) {
+    if (i >= items) {
+      // This group's list is done: take from the next group's.
+      if (++tried == 8) break;
+      grp = (grp + 1) & 7;
+      group();
       ++r;
-      if (threadIdx.x == 0) s_item[r & 1] = next;
+      if (threadIdx.x == 0) s_item[r & 1] = (int)sched_take(base + grp * kSchedStride);
       __syncthreads();
       i = s_item[r & 1];
+      continue;
     }
-    // Every workgroup of the launch has taken its last number once all have counted themselves out.
-    if (threadIdx.x == 0 && sched_take(base + 8 * kSchedStride) == (uint32_t)(total - 1)) {
-      for (int x = 0; x <= 8; ++x)
-        __hip_atomic_exchange(base + x * kSchedStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
+    int next = 0;
+    const int g = i / (2 * num_qtiles), gp = min(2, cnt - 2 * g), j = i - g * 2 * num_qtiles;
+    varlen_item<true>(q, k, v, cu_seqlens, H, KV, scale_log2, out, lo + 2 * g + j % gp,
+                         num_qtiles - 1 - j / gp, s_k0, s_k1, s_v0, s_v1, base + grp * kSchedStride, &next);
+    ++r;
+    if (threadIdx.x == 0) s_item[r & 1] = next;
+    __syncthreads();
+    i = s_item[r & 1];
+  }
+  // Every workgroup of the launch has taken its last number once all have counted themselves out.
+  if (threadIdx.x == 0 && sched_take(base + 8 * kSchedStride) == (uint32_t)(total - 1)) {
+    for (int x = 0; x <= 8; ++x)
+      __hip_atomic_exchange(base + x * kSchedStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -642,32 +639,25 @@ extern "C" int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const 
   OXR_RETURN_IF(!q || !k || !v || !cu_seqlens || !out, OXR_ERR_INVALID_ARG);
   OXR_RETURN_IF(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 != 0 || (uintptr_t)out % 8 != 0,
                 OXR_ERR_UNSUPPORTED);
-  // Bidirectional prefill runs the ping-pong kernel; the causal form of that kernel needs more
-  // registers than two waves per SIMD have (it spills), so causal prefill runs the 4-wave kernel.
-  const bool pingpong = !causal;
-  const int rows_per_head = (pingpong ? kPRows : kVRows) / G;
+  // Bidirectional prefill runs the ping-pong kernel; its causal form needs more registers than two
+  // waves per SIMD have (it spills), so causal prefill runs the persistent 4-wave kernel.
+  const int rows_per_head = (causal ? kVRows : kPRows) / G;
   const int num_qtiles = (max_len + rows_per_head - 1) / rows_per_head;
   OXR_RETURN_IF((int64_t)num_qtiles * num_kv_heads * num_seqs > INT32_MAX, OXR_ERR_UNSUPPORTED);
-  const dim3 grid((unsigned)(num_qtiles * num_kv_heads * num_seqs));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   const int num_pairs = num_seqs * num_kv_heads;
-  static std::atomic<uint32_t> launches{0};
-  if (pingpong) {
+  if (!causal) {
+    const dim3 grid((unsigned)(num_qtiles * num_pairs));
     hipLaunchKernelGGL(varlen_attention_pp_kernel<false>, grid, dim3(64 * kPWaves), 0, s, q, k, v, cu_seqlens,
                        num_heads, num_kv_heads, num_qtiles, scale_log2, out);
-  } else if (causal && num_pairs % 8 == 0) {
-    // Persistent: two workgroups per CU of the 256, or fewer when an XCD has fewer items.
-    const int per_xcd = (int)std::min<int64_t>(kPersistentSlots, (int64_t)(num_pairs / 8) * num_qtiles);
-    const int ring = (int)(launches.fetch_add(1u, std::memory_order_relaxed) % kSchedRing);
-    hipLaunchKernelGGL((varlen_attention_kernel<true, true>), dim3(8 * per_xcd), dim3(64 * kVWaves), 0, s, q, k, v,
-                       cu_seqlens, num_heads, num_kv_heads, num_qtiles, num_pairs, ring, scale_log2, out);
-  } else if (causal) {
-    hipLaunchKernelGGL((varlen_attention_kernel<true, false>), grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
-                       num_heads, num_kv_heads, num_qtiles, num_pairs, 0, scale_log2, out);
   } else {
-    hipLaunchKernelGGL((varlen_attention_kernel<false, false>), grid, dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
-                       num_heads, num_kv_heads, num_qtiles, num_pairs, 0, scale_log2, out);
+    // Two workgroups per CU, or fewer when the largest XCD group has fewer items.
+    static std::atomic<uint32_t> launches{0};
+    const int ring = (int)(launches.fetch_add(1u, std::memory_order_relaxed) % kSchedRing);
+    const int per_xcd = (int)std::min<int64_t>(kPersistentSlots, (int64_t)((num_pairs + 7) / 8) * num_qtiles);
+    hipLaunchKernelGGL(varlen_attention_kernel, dim3(8 * per_xcd), dim3(64 * kVWaves), 0, s, q, k, v, cu_seqlens,
+                       num_heads, num_kv_heads, num_qtiles, num_pairs, ring, scale_log2, out);
   }
   return OXR_LAUNCH_STATUS();
 }

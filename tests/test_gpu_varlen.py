@@ -4,7 +4,8 @@
 lengths around the 16-row query and 64-key tile edges, an empty sequence, one-token sequences,
 causal and bidirectional, every supported head grouping (1, 2, 4 and 8 q heads per kv head),
 prefill-sized sequences, and the persistent causal launch (pairs divisible by 8) over several
-rounds of items per workgroup, replayed from a captured graph and run on two streams at once.
+rounds of items per workgroup, fewer pairs than XCD groups, replayed from a captured graph and run
+on two streams at once.
 """
 
 from __future__ import annotations
@@ -67,6 +68,13 @@ def test_persistent_rounds(lens) -> None:
     # several rounds of items per workgroup, ragged and empty sequences, and (3 sequences: 3 pairs
     # per XCD) a last pair group of one.
     _case(lens, 32, 8, True, seed=30 + len(lens))
+
+
+@pytest.mark.parametrize("lens,H,KV", [([1000], 8, 1), ([513, 7], 4, 2), ([300, 1, 77], 8, 4)])
+def test_causal_few_pairs(lens, H, KV) -> None:
+    # Fewer (sequence, kv head) pairs than XCD groups: the empty groups' workgroups take every item
+    # from the other groups' lists.
+    _case(lens, H, KV, True, seed=50 + len(lens))
 
 
 def _inputs(lens, H, KV, seed):
