@@ -97,23 +97,22 @@ __device__ __forceinline__ float row_max32(const f32x16 (&sv)[2]) {
   return fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
 }
 
-// One work item: query tile `qt` (128 / G positions of each of the G q heads) of (sequence, kv head)
-// pair `pair`.  Every wave of the workgroup takes part (it ends with a workgroup barrier and touches no
-// LDS after it, so the next item may start right away).  With a counter `ctr`, thread 0 takes the next
-// item number from it into `next` when the item's last two key tiles begin (or at once if it has no
+// One causal work item: query tile `qt` (128 / G positions of each of the G q heads) of (sequence, kv
+// head) pair `pair`.  Every wave of the workgroup takes part (it ends with a workgroup barrier and touches
+// no LDS after it, so the next item may start right away).  Thread 0 takes the next item number from
+// the counter `ctr` into `next` when the item's last two key tiles begin (or at once if it has no
 // work), late enough that the items are started in list order.
-template <bool kCausal>
 __device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                             const bf16_t* __restrict__ v, const int32_t* __restrict__ cu_seqlens,
                                             int H, int KV, float scale_log2, bf16_t* __restrict__ out, int pair,
                                             int qt, bf16_t* s_k0, bf16_t* s_k1, bf16_t* s_v0, bf16_t* s_v1,
-                                            uint32_t* ctr = nullptr, int* next = nullptr) {
+                                            uint32_t* ctr, int* next) {
   const int seq = pair / KV, kvh = pair - seq * KV;
   const int start = cu_seqlens[seq], len = cu_seqlens[seq + 1] - start;
   const int G = H / KV, rph = kVRows / G;  // positions per head in this workgroup
   const int q0 = qt * rph;                 // first position, per head
   if (q0 >= len) {                         // whole workgroup: before any barrier
-    if (ctr != nullptr && threadIdx.x == 0) *next = (int)sched_take(ctr);
+    if (threadIdx.x == 0) *next = (int)sched_take(ctr);
     return;
   }
 
@@ -126,7 +125,7 @@ __device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const 
   // The wave's positions: offsets first_off .. first_off + min(rph, 32) - 1 from q0.
   const int first_off = rph >= 32 ? (32 * wave) % rph : 0;
   const int wave_first = q0 + first_off;
-  const int wave_last = kCausal ? min(wave_first + min(rph, 32) - 1, len - 1) : len - 1;
+  const int wave_last = min(wave_first + min(rph, 32) - 1, len - 1);
 
   // Q^T fragments (B operand): lane (n, h) holds Q[qpos][16i + 8h, +8) for dim step i.
   u32x4 qf[8];
@@ -142,7 +141,7 @@ __device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const 
 #pragma unroll
   for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(qf[i]));
 
-  const int key_end = kCausal ? min(len, q0 + rph) : len;  // keys this workgroup needs
+  const int key_end = min(len, q0 + rph);  // keys this workgroup needs
   const int tiles = (key_end + kKeyTile - 1) / kKeyTile;
 
   // Key tiles go straight from memory to LDS (global_load_lds, 16 bytes per lane: lane i of an
@@ -209,14 +208,14 @@ __device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const 
     const int kt0 = t * kKeyTile;
     if (kt0 <= wave_last) {  // wave-uniform: otherwise every key of this and later tiles is masked
       // wave-uniform: a tile crossing the diagonal of one of the wave's rows, or the sequence end
-      const bool edge = (kCausal && kt0 + kKeyTile - 1 > wave_first) || kt0 + kKeyTile > len;
+      const bool edge = kt0 + kKeyTile - 1 > wave_first || kt0 + kKeyTile > len;
       if (edge) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int key = kt0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (key >= len || (kCausal && key > qpos)) cur[kb][e] = -INFINITY;
+            if (key >= len || key > qpos) cur[kb][e] = -INFINITY;
           }
       }
       // Row maximum (exact in any order) as a tree of three-input maxima (v_max3_f32): 32 scores in
@@ -279,7 +278,7 @@ __device__ __forceinline__ void varlen_item(const bf16_t* __restrict__ q, const 
   __syncthreads();
   qk(s_k0, sa);
   for (int t = 0; t < tiles; t += 2) {
-    if (ctr != nullptr && t + 2 >= tiles && threadIdx.x == 0) *next = (int)sched_take(ctr);
+    if (t + 2 >= tiles && threadIdx.x == 0) *next = (int)sched_take(ctr);
     step(t, sa, sb, s_k1, s_v0, s_k0, s_v1);
     if (t + 1 < tiles) step(t + 1, sb, sa, s_k0, s_v1, s_k1, s_v0);
   }
@@ -351,7 +350,7 @@ __global__ __launch_bounds__(64 * kVWaves, 2) void varlen_attention_kernel(
     }
     int next = 0;
     const int g = i / (2 * num_qtiles), gp = min(2, cnt - 2 * g), j = i - g * 2 * num_qtiles;
-    varlen_item<true>(q, k, v, cu_seqlens, H, KV, scale_log2, out, lo + 2 * g + j % gp,
+    varlen_item(q, k, v, cu_seqlens, H, KV, scale_log2, out, lo + 2 * g + j % gp,
                          num_qtiles - 1 - j / gp, s_k0, s_k1, s_v0, s_v1, base + grp * kSchedStride, &next);
     ++r;
     if (threadIdx.x == 0) s_item[r & 1] = next;
