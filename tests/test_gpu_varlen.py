@@ -5,7 +5,8 @@ lengths around the 16-row query and 64-key tile edges, an empty sequence, one-to
 causal and bidirectional, every supported head grouping (1, 2, 4 and 8 q heads per kv head),
 prefill-sized sequences, and the persistent causal launch (pairs divisible by 8) over several
 rounds of items per workgroup, fewer pairs than XCD groups, replayed from a captured graph and run
-on two streams at once.
+on two streams at once; and at the benchmark's prefill shapes, rows at the start, middle and end of
+every sequence against the oracle.
 """
 
 from __future__ import annotations
@@ -16,6 +17,7 @@ import torch
 
 from conftest import announce, pkg
 from oracle import attention as oracle_attention
+from oracle import bf16
 
 pytestmark = pytest.mark.gpu
 attention = pkg("attention")
@@ -75,6 +77,39 @@ def test_causal_few_pairs(lens, H, KV) -> None:
     # Fewer (sequence, kv head) pairs than XCD groups: the empty groups' workgroups take every item
     # from the other groups' lists.
     _case(lens, H, KV, True, seed=50 + len(lens))
+
+
+@pytest.mark.parametrize("lens", [[4096] * 8, np.random.default_rng(0).integers(1, 4097, 32).tolist()],
+                         ids=["8x4096", "32 mixed lengths"])
+def test_causal_full_size_rows(lens) -> None:
+    # The benchmark's prefill shapes (16 q heads over 8 kv heads, 8 x 4096 and 32 mixed lengths up to
+    # 4096): every row is written, and blocks of 8 query rows at the start, middle and end of each
+    # sequence match the oracle (the oracle on those rows only: a block of rows [p0, p1) over keys
+    # [0, p1) with its end-aligned causal mask is exactly their causal attention).
+    H, KV = 16, 8
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    g = torch.Generator(device="cuda").manual_seed(60 + len(lens))
+    q = torch.randn(T, H, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(T, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(T, KV, 128, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.full_like(q, float("nan"))
+    announce("varlen full size", f"{len(lens)} seqs, {T} tokens")
+    attention.varlen(q, k, v, torch.from_numpy(cu).cuda(), max(lens), causal=True, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all()), "rows left unwritten"
+    qb, kb, vb = _bits(q), _bits(k), _bits(v)
+    got_all = out.float().cpu().numpy()
+    for i, n in enumerate(lens):
+        start = int(cu[i])
+        for p0 in sorted({0, max(0, n // 2 - 4), max(0, n - 8)}):
+            p1 = min(n, p0 + 8)
+            exact = oracle_attention.attend(bf16.to_f32(qb[start + p0:start + p1]), bf16.to_f32(kb[start:start + p1]),
+                                            bf16.to_f32(vb[start:start + p1]), 128 ** -0.5, causal=True)
+            got = got_all[start + p0:start + p1]
+            err = np.abs(got - exact)
+            bound = ATOL + RTOL * np.abs(exact)
+            assert (err <= bound).all(), f"seq {i} rows [{p0}, {p1}): max err {err.max():.3g}"
 
 
 def _inputs(lens, H, KV, seed):
