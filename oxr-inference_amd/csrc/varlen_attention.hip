@@ -642,7 +642,10 @@ extern "C" int oxr_varlen_attention(const oxr_bf16* q, const oxr_bf16* k, const 
   // waves per SIMD have (it spills), so causal prefill runs the persistent 4-wave kernel.
   const int rows_per_head = (causal ? kVRows : kPRows) / G;
   const int num_qtiles = (max_len + rows_per_head - 1) / rows_per_head;
-  OXR_RETURN_IF((int64_t)num_qtiles * num_kv_heads * num_seqs > INT32_MAX, OXR_ERR_UNSUPPORTED);
+  // Item numbers are int: the counters run past a list's end by at most one number per workgroup and
+  // group, so the lists keep that much headroom below INT32_MAX.
+  OXR_RETURN_IF((int64_t)num_qtiles * num_kv_heads * num_seqs > INT32_MAX - 8 * 8 * kPersistentSlots,
+                OXR_ERR_UNSUPPORTED);
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   const int num_pairs = num_seqs * num_kv_heads;
